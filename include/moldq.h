@@ -1,0 +1,132 @@
+/*
+ * moldq.h — C ABI of the MI355X (gfx950) GGUF quantized-linear library.
+ *
+ * This is the drop-in boundary for candle's quantized device arm
+ * (candle-core-mold 0.9.10, pinned at /root/reference/Cargo.lock:507-535):
+ * a Rust `QStorage::Rocm(QRocmStorage)` arm calls these functions the way
+ * `QCudaStorage` calls candle's CUDA kernels.  Plain pointers and sizes only.
+ *
+ * Conventions
+ *   - A weight is a GGUF tensor of `n` rows (output features) by `k` columns
+ *     (input features, GGUF ne[0]); each row is k/block_size consecutive
+ *     blocks.  The layer computes y[m, n] = x[m, k] . W[n, k]^T (+ bias[n]).
+ *   - Return value 0 is success; a negative MQ_E_* code is failure and
+ *     mq_last_error() returns a thread-local message.  Nothing aborts or
+ *     throws across the ABI.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL is the null stream)
+ *     and is asynchronous unless stated otherwise.
+ *   - A context is bound to one device; call it from one thread at a time.
+ *     Its scratch buffer is shared by every call on that context, so calls
+ *     that use scratch must be ordered on one stream.
+ */
+#ifndef MOLDQ_H
+#define MOLDQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOLDQ_VERSION 1
+
+/* ggml / GGUF tensor type ids (candle `GgmlDType`). */
+typedef enum mq_dtype {
+    MQ_F32 = 0, MQ_F16 = 1, MQ_Q4_0 = 2, MQ_Q4_1 = 3, MQ_Q5_0 = 6, MQ_Q5_1 = 7,
+    MQ_Q8_0 = 8, MQ_Q2_K = 10, MQ_Q3_K = 11, MQ_Q4_K = 12, MQ_Q5_K = 13,
+    MQ_Q6_K = 14, MQ_BF16 = 30
+} mq_dtype;
+
+enum {
+    MQ_OK = 0,
+    MQ_E_INVALID = -1,      /* bad argument: dtype, shape, k % block, null pointer */
+    MQ_E_HIP = -2,          /* HIP runtime error */
+    MQ_E_OOM = -3,          /* device or host allocation failed */
+    MQ_E_UNSUPPORTED = -4,  /* valid request this build does not implement */
+    MQ_E_IO = -5            /* file read / format error (GGUF) */
+};
+
+/* Epilogue applied to x.W^T + bias before the store. */
+typedef enum mq_act { MQ_ACT_NONE = 0, MQ_ACT_GELU_TANH = 1 } mq_act;
+
+typedef struct mq_ctx mq_ctx;
+typedef struct mq_qtensor mq_qtensor;
+typedef struct mq_gguf mq_gguf;
+
+/* Thread-local description of the last failure on this thread. */
+const char *mq_last_error(void);
+int mq_version(void);
+
+/* GgmlDType::block_size() / type_size(): elements and bytes per block.
+ * Replaces candle's GgmlDType methods used at
+ * crates/mold-inference/src/flux/pipeline.rs:198.  Return 0 for unknown ids. */
+int mq_block_size(int dtype);
+int mq_type_size(int dtype);
+
+/* Device context (candle Device::new_cuda(ordinal), device.rs:165). */
+int mq_ctx_create(int device_ordinal, mq_ctx **out);
+void mq_ctx_destroy(mq_ctx *ctx);
+/* Pre-allocate one HBM arena that later uploads are carved from (bump
+ * allocation, released with the context).  Optional. */
+int mq_ctx_reserve_arena(mq_ctx *ctx, size_t bytes);
+/* Pre-size the scratch buffer used for f32->bf16 activation staging so that
+ * mq_qmatmul never allocates.  Optional. */
+int mq_ctx_reserve_scratch(mq_ctx *ctx, size_t bytes);
+
+/* Upload a GGUF weight (blocks exactly as stored in the file) to the device.
+ * Replaces QCudaStorage load_quantized / `content.tensor(reader, name, device)`
+ * (crates/mold-inference/src/flux/lora.rs:722) and VarBuilder::from_gguf
+ * (crates/mold-inference/src/flux/pipeline.rs:976).  Synchronous: the host
+ * buffer may be reused on return.  nbytes must equal n*k/bs*type_size. */
+int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
+                      const void *host_blocks, size_t nbytes, mq_qtensor **out);
+/* Same from GGUF blocks already in device memory (copied; caller keeps its
+ * buffer).  Ordered on `stream`. */
+int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
+                           const void *dev_blocks, size_t nbytes, void *stream,
+                           mq_qtensor **out);
+/* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
+ * Synchronous. */
+int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes);
+void mq_qtensor_free(mq_qtensor *w);
+/* QTensor::dtype() / shape / storage_size_in_bytes(). */
+int mq_qtensor_info(const mq_qtensor *w, int *dtype, int64_t *n, int64_t *k,
+                    size_t *gguf_bytes, size_t *device_bytes);
+
+/* QTensor::dequantize(&device) -> dense [n, k] in dst_dtype (F32, F16 or
+ * BF16) at dst (row-major, k contiguous).  F32 output is bit-exact with the
+ * GGUF formulas; F16/BF16 are that value rounded to nearest even.
+ * Replaces candle's dequantize / dequantize_f16 (called at
+ * crates/mold-inference/src/qwen_image/quantized_transformer.rs:62-66). */
+int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, void *stream);
+
+/* QMatMul::forward (+ quantized_nn::Linear bias, optional GELU-tanh):
+ * y[m, :n] = act(x[m, :k] . W^T + bias).  x_dtype F32 or BF16 with row
+ * stride ldx (elements); y_dtype F32 or BF16 with row stride ldy.  bias is
+ * f32 [n] or NULL.  Picks the skinny GEMV for small m and the fused
+ * dequant-MFMA GEMM otherwise.  Replaces QCudaStorage::fwd, reached from
+ * crates/mold-inference/src/flux2/quantized_transformer.rs:40-45 and the FLUX
+ * quantized model's linears. */
+int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
+               int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
+               const float *bias, int act, void *stream);
+
+/* --- GGUF v2/v3 reader (candle gguf_file::Content::read, used at
+ *     crates/mold-inference/src/flux/pipeline.rs:286-287). ------------------- */
+int mq_gguf_open(const char *path, mq_gguf **out);
+void mq_gguf_close(mq_gguf *g);
+int64_t mq_gguf_tensor_count(const mq_gguf *g);
+/* Index of a tensor by name, or -1. */
+int64_t mq_gguf_find(const mq_gguf *g, const char *name);
+/* dims[0] is GGUF ne[0] (the contiguous axis). *name stays valid until close. */
+int mq_gguf_tensor_info(const mq_gguf *g, int64_t index, const char **name, int *dtype,
+                        int *n_dims, int64_t dims[4], uint64_t *file_offset, size_t *nbytes);
+/* Read a 2-D quantized tensor from the file and upload it (content.tensor(
+ * reader, name, device)). */
+int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOLDQ_H */

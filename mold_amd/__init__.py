@@ -1,0 +1,11 @@
+"""mold_amd — MI355X-native (gfx950) GGUF quantized-linear hot path for mold.
+
+The product is libmoldq.so (HIP kernels behind the C ABI in include/moldq.h).
+This package is the host-side mirror of candle's quantized API used by the
+tests and the benchmark; see quantized.py and gguf.py.
+"""
+from ._lib import MoldqError, load  # noqa: F401
+from .quantized import ACT_GELU_TANH, ACT_NONE, Device, GgmlDType, Linear, QMatMul, QTensor, QUANT_TYPES  # noqa: F401
+
+__all__ = ["MoldqError", "load", "Device", "GgmlDType", "Linear", "QMatMul", "QTensor", "QUANT_TYPES",
+           "ACT_NONE", "ACT_GELU_TANH"]

@@ -1,0 +1,47 @@
+// mq_kernels.h — launchers shared between the kernel files and the C ABI.
+#pragma once
+
+#include "mq_common.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace mq {
+
+hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, bool inverse,
+                         hipStream_t stream);
+hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
+                          hipStream_t stream);
+// bf16 [m, k] (row stride ldx) -> f32 [m, k] contiguous, for the GEMV.
+hipError_t launch_widen_bf16(const __bf16 *x, int64_t m, int64_t k, int64_t ldx, float *out,
+                             hipStream_t stream);
+hipError_t launch_stage_bf16(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, __bf16 *out,
+                             int64_t kp, hipStream_t stream);
+
+// Skinny-M GEMV (m <= kGemvMaxM).  `partial` is scratch of
+// ksplit*m*ntiles*64 floats when the launcher decides to split K (it returns
+// the bytes it needs through gemv_scratch_bytes first).
+constexpr int kGemvMaxM = 8;
+size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const float *x, int64_t m,
+                       int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
+                       float *partial, hipStream_t stream);
+
+// Fused dequant -> LDS -> bf16 MFMA GEMM.  a is bf16 [m, lda] with lda a
+// multiple of 64 covering ceil(k/64)*64 zero-padded columns.
+hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w,
+                       const __bf16 *a, int64_t m, int64_t lda, void *y, int y_type, int64_t ldy,
+                       const float *bias, int act, hipStream_t stream);
+
+// Epilogue activation (GELU with the tanh approximation, as candle's gelu()).
+__device__ __forceinline__ float apply_act(float v, int act) {
+  if (act == 1) {
+    const float c = 0.7978845608028654f;  // sqrt(2/pi)
+    return 0.5f * v * (1.0f + tanhf(c * (v + 0.044715f * v * v * v)));
+  }
+  return v;
+}
+
+}  // namespace mq

@@ -1,0 +1,173 @@
+// mq_layout.hip — GGUF blocks <-> device tiled-planar layout (see mq_common.h),
+// dense dequantize, and the f32 -> bf16 activation staging used by the GEMM.
+#include "mq_kernels.h"
+
+namespace mq {
+
+// One thread per GGUF byte (grid-stride).  inverse=false: raw -> tiled;
+// inverse=true: tiled -> raw.  Upload/download only, never on the hot path.
+template <int TYPE>
+__global__ void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, Geo g,
+                              int64_t total, int inverse) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  const int64_t row_bytes = g.nb * ti.ts;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / row_bytes;
+    const int64_t rem = i - n * row_bytes;
+    const int64_t b = rem / ti.ts;
+    const int j = (int)(rem - b * ti.ts);
+    int f = 0;
+#pragma unroll
+    for (int q = 1; q < ti.nf; ++q)
+      if (j >= ti.f[q].off) f = q;
+    const int64_t off = field_offset(g.plane[f], ti.f[f].size, g.nb, n / kRowTile, b,
+                                     (int)(n % kRowTile), j - ti.f[f].off);
+    if (inverse) dst[i] = src[off];
+    else dst[off] = src[i];
+  }
+}
+
+hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, bool inverse,
+                         hipStream_t stream) {
+  const TypeInfo ti = type_info(type);
+  const int64_t total = g.n * g.nb * ti.ts;
+  if (total == 0) return hipSuccess;
+  const int threads = 256;
+  const int64_t want = (total + threads - 1) / threads;
+  const int blocks = (int)(want < 65536 ? want : 65536);
+  bool ok = dispatch_type(type, [&]<int T>() {
+    hipLaunchKernelGGL(repack_kernel<T>, dim3(blocks), dim3(threads), 0, stream,
+                       static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), g, total,
+                       inverse ? 1 : 0);
+  });
+  if (!ok) return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------- dequantize
+
+template <typename OUT>
+__device__ __forceinline__ void store8(OUT *dst, const float v[8]);
+
+template <>
+__device__ __forceinline__ void store8<float>(float *dst, const float v[8]) {
+  reinterpret_cast<float4 *>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4 *>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <>
+__device__ __forceinline__ void store8<__bf16>(__bf16 *dst, const float v[8]) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)v[i];
+  *reinterpret_cast<bf16x8 *>(dst) = r;
+}
+
+template <>
+__device__ __forceinline__ void store8<_Float16>(_Float16 *dst, const float v[8]) {
+  f16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (_Float16)v[i];
+  *reinterpret_cast<f16x8 *>(dst) = r;
+}
+
+// One thread per 8 consecutive outputs of a row; consecutive threads write
+// consecutive 8-element groups (coalesced stores, the dominant traffic).
+template <int TYPE, typename OUT>
+__global__ void dequant_kernel(WView w, int64_t n, int64_t k, OUT *__restrict__ dst) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  const int64_t groups_per_row = k >> 3;
+  const int64_t total = n * groups_per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / groups_per_row;
+    const int64_t kk = (i - row * groups_per_row) << 3;
+    const int64_t b = kk / ti.bs;
+    const int e0 = (int)(kk - b * ti.bs);
+    float v[8];
+    decode8<TYPE>(w, row / kRowTile, (int)(row % kRowTile), b, e0, v);
+    store8<OUT>(dst + row * k + kk, v);
+  }
+}
+
+hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
+                          hipStream_t stream) {
+  const int64_t total = n * (k >> 3);
+  if (total == 0) return hipSuccess;
+  const int threads = 256;
+  const int64_t want = (total + threads - 1) / threads;
+  const int blocks = (int)(want < 262144 ? want : 262144);
+  bool ok = dispatch_type(type, [&]<int T>() {
+    if (dst_type == F32)
+      hipLaunchKernelGGL((dequant_kernel<T, float>), dim3(blocks), dim3(threads), 0, stream, w, n, k,
+                         static_cast<float *>(dst));
+    else if (dst_type == BF16)
+      hipLaunchKernelGGL((dequant_kernel<T, __bf16>), dim3(blocks), dim3(threads), 0, stream, w, n, k,
+                         static_cast<__bf16 *>(dst));
+    else
+      hipLaunchKernelGGL((dequant_kernel<T, _Float16>), dim3(blocks), dim3(threads), 0, stream, w, n,
+                         k, static_cast<_Float16 *>(dst));
+  });
+  if (!ok) return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// ------------------------------------------------- activation staging (GEMM A)
+
+// x[m, k] (f32 or bf16, row stride ldx) -> bf16 [m, kp] with zeros in
+// columns k..kp-1.  One thread per 8 output columns.
+template <typename IN>
+__global__ void stage_bf16_kernel(const IN *__restrict__ x, int64_t m, int64_t k, int64_t ldx,
+                                  __bf16 *__restrict__ out, int64_t kp) {
+  const int64_t gpr = kp >> 3;
+  const int64_t total = m * gpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / gpr;
+    const int64_t c = (i - row * gpr) << 3;
+    bf16x8 r;
+    const IN *src = x + row * ldx + c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = (c + j < k) ? (__bf16)(float)src[j] : (__bf16)0.0f;
+    *reinterpret_cast<bf16x8 *>(out + row * kp + c) = r;
+  }
+}
+
+hipError_t launch_stage_bf16(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, __bf16 *out,
+                             int64_t kp, hipStream_t stream) {
+  const int64_t total = m * (kp >> 3);
+  if (total == 0) return hipSuccess;
+  const int threads = 256;
+  const int64_t want = (total + threads - 1) / threads;
+  const int blocks = (int)(want < 262144 ? want : 262144);
+  if (x_type == F32)
+    hipLaunchKernelGGL(stage_bf16_kernel<float>, dim3(blocks), dim3(threads), 0, stream,
+                       static_cast<const float *>(x), m, k, ldx, out, kp);
+  else
+    hipLaunchKernelGGL(stage_bf16_kernel<__bf16>, dim3(blocks), dim3(threads), 0, stream,
+                       static_cast<const __bf16 *>(x), m, k, ldx, out, kp);
+  return hipGetLastError();
+}
+
+__global__ void widen_bf16_kernel(const __bf16 *__restrict__ x, int64_t m, int64_t k, int64_t ldx,
+                                  float *__restrict__ out) {
+  const int64_t total = m * k;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / k, c = i - row * k;
+    out[i] = (float)x[row * ldx + c];
+  }
+}
+
+hipError_t launch_widen_bf16(const __bf16 *x, int64_t m, int64_t k, int64_t ldx, float *out,
+                             hipStream_t stream) {
+  const int64_t total = m * k;
+  if (total == 0) return hipSuccess;
+  const int64_t want = (total + 255) / 256;
+  const int blocks = (int)(want < 65536 ? want : 65536);
+  hipLaunchKernelGGL(widen_bf16_kernel, dim3(blocks), dim3(256), 0, stream, x, m, k, ldx, out);
+  return hipGetLastError();
+}
+
+}  // namespace mq

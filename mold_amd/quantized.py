@@ -1,0 +1,244 @@
+"""Host-side mirror of candle's quantized API, backed by libmoldq's HIP kernels.
+
+Names, argument meaning and error behaviour follow candle-core-mold 0.9.10's
+`quantized` module and candle-transformers-mold's `quantized_nn` (pinned at
+/root/reference/Cargo.lock:507-597), as mold calls them:
+
+  GgmlDType.block_size()          flux/pipeline.rs:198
+  QTensor.dtype() / dequantize()  flux/lora.rs:759,765; qwen_image/quantized_transformer.rs:62-66
+  QMatMul.forward(x)              flux2/quantized_transformer.rs:40-45 (via Linear)
+  Linear(weight, bias)            qwen_image/quantized_transformer.rs:89 (Linear::from_arc)
+  Device(ordinal)                 device.rs:165 (Device::new_cuda)
+
+(paths under /root/reference/crates/mold-inference/src).  torch tensors are
+only the carrier for device memory and streams; every computation is a
+libmoldq call.  Errors raise MoldqError (candle returns Err(..)).
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import check
+
+
+class GgmlDType(enum.IntEnum):
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
+    Q8_0 = 8
+    Q2_K = 10
+    Q3_K = 11
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+    BF16 = 30
+
+    def block_size(self) -> int:
+        return _lib.load().mq_block_size(int(self))
+
+    def type_size(self) -> int:
+        return _lib.load().mq_type_size(int(self))
+
+    @property
+    def is_quantized(self) -> bool:
+        return self.block_size() > 1
+
+
+QUANT_TYPES = [GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_1, GgmlDType.Q8_0,
+               GgmlDType.Q2_K, GgmlDType.Q3_K, GgmlDType.Q4_K, GgmlDType.Q5_K, GgmlDType.Q6_K]
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_ptr(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class Device:
+    """One GPU (libmoldq context).  candle: Device::new_cuda(ordinal)."""
+
+    def __init__(self, ordinal: int = 0):
+        lib = _lib.load()
+        h = ctypes.c_void_p()
+        check(lib.mq_ctx_create(ordinal, ctypes.byref(h)))
+        self._h = h
+        self.ordinal = ordinal
+
+    @property
+    def handle(self) -> ctypes.c_void_p:
+        return self._h
+
+    def reserve_arena(self, nbytes: int) -> None:
+        check(_lib.load().mq_ctx_reserve_arena(self._h, nbytes))
+
+    def reserve_scratch(self, nbytes: int) -> None:
+        check(_lib.load().mq_ctx_reserve_scratch(self._h, nbytes))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().mq_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _dtype_code(dt) -> int:
+    torch = _torch()
+    if dt in (torch.float32, "f32", GgmlDType.F32):
+        return int(GgmlDType.F32)
+    if dt in (torch.bfloat16, "bf16", GgmlDType.BF16):
+        return int(GgmlDType.BF16)
+    if dt in (torch.float16, "f16", GgmlDType.F16):
+        return int(GgmlDType.F16)
+    raise ValueError(f"unsupported dtype {dt}")
+
+
+class QTensor:
+    """A device-resident GGUF weight [n, k] (rows = output features)."""
+
+    def __init__(self, device: Device, handle: ctypes.c_void_p):
+        self.device = device
+        self._h = handle
+        lib = _lib.load()
+        dt, n, k = ctypes.c_int(), ctypes.c_int64(), ctypes.c_int64()
+        gb, db = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib.mq_qtensor_info(handle, ctypes.byref(dt), ctypes.byref(n), ctypes.byref(k),
+                                  ctypes.byref(gb), ctypes.byref(db)))
+        self._dtype = GgmlDType(dt.value)
+        self.shape = (n.value, k.value)
+        self._gguf_bytes = gb.value
+        self.device_bytes = db.value
+
+    # candle: QTensor::quantize is CPU-side fixture generation here (oracle);
+    # loading GGUF blocks is the upload path below.
+    @classmethod
+    def from_blocks(cls, device: Device, dtype: GgmlDType, shape: Sequence[int], blocks) -> "QTensor":
+        """Upload GGUF blocks from host memory (bytes / numpy uint8)."""
+        n, k = int(shape[0]), int(shape[1])
+        buf = np.ascontiguousarray(np.frombuffer(blocks, dtype=np.uint8) if isinstance(blocks, (bytes, bytearray))
+                                   else np.asarray(blocks, dtype=np.uint8)).reshape(-1)
+        h = ctypes.c_void_p()
+        check(_lib.load().mq_qtensor_upload(device.handle, int(dtype), n, k, buf.ctypes.data, buf.nbytes,
+                                            ctypes.byref(h)))
+        return cls(device, h)
+
+    @classmethod
+    def from_device_blocks(cls, device: Device, dtype: GgmlDType, shape: Sequence[int], blocks_tensor,
+                           stream=None) -> "QTensor":
+        """Build from GGUF blocks already in device memory (a uint8 torch tensor)."""
+        n, k = int(shape[0]), int(shape[1])
+        h = ctypes.c_void_p()
+        check(_lib.load().mq_qtensor_from_device(device.handle, int(dtype), n, k, blocks_tensor.data_ptr(),
+                                                 blocks_tensor.numel() * blocks_tensor.element_size(),
+                                                 _stream_ptr(stream), ctypes.byref(h)))
+        return cls(device, h)
+
+    def dtype(self) -> GgmlDType:
+        return self._dtype
+
+    def storage_size_in_bytes(self) -> int:
+        return self._gguf_bytes
+
+    def data(self) -> np.ndarray:
+        """GGUF blocks read back from the device (byte-identical to the upload)."""
+        out = np.empty(self._gguf_bytes, dtype=np.uint8)
+        check(_lib.load().mq_qtensor_download(self.device.handle, self._h, out.ctypes.data, out.nbytes))
+        return out
+
+    def dequantize(self, dtype=None, out=None, stream=None):
+        """Dense [n, k] torch tensor on the device (f32 by default, or f16/bf16)."""
+        torch = _torch()
+        dtype = torch.float32 if dtype is None else dtype
+        if out is None:
+            out = torch.empty(self.shape, dtype=dtype, device=f"cuda:{self.device.ordinal}")
+        assert out.is_contiguous() and tuple(out.shape) == self.shape and out.dtype == dtype
+        check(_lib.load().mq_dequantize(self.device.handle, self._h, out.data_ptr(), _dtype_code(dtype),
+                                        _stream_ptr(stream)))
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            _lib.load().mq_qtensor_free(self._h)
+            self._h = None
+
+    @property
+    def handle(self):
+        return self._h
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+ACT_NONE, ACT_GELU_TANH = 0, 1
+
+
+class QMatMul:
+    """candle QMatMul: y = x . W^T with W a QTensor; x [..., k] on the device."""
+
+    def __init__(self, w: QTensor):
+        self.w = w
+
+    @classmethod
+    def from_qtensor(cls, w: QTensor) -> "QMatMul":
+        return cls(w)
+
+    def forward(self, x, bias=None, act: int = ACT_NONE, out_dtype=None, out=None, stream=None):
+        torch = _torch()
+        n, k = self.w.shape
+        if x.shape[-1] != k:
+            raise ValueError(f"QMatMul: x last dim {x.shape[-1]} != weight k {k}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, k)
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        m = x2.shape[0]
+        out_dtype = x.dtype if out_dtype is None else out_dtype
+        if out is None:
+            out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+        else:
+            assert out.dtype == out_dtype and tuple(out.shape) == (m, n)
+        if bias is not None:
+            assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == n
+        check(_lib.load().mq_qmatmul(self.w.device.handle, self.w.handle, x2.data_ptr(), _dtype_code(x2.dtype), m,
+                                     x2.stride(0), out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
+                                     bias.data_ptr() if bias is not None else None, int(act), _stream_ptr(stream)))
+        return out.reshape(*lead, n)
+
+    __call__ = forward
+
+
+class Linear:
+    """candle-transformers quantized_nn::Linear: QMatMul plus optional f32 bias."""
+
+    def __init__(self, weight: QTensor, bias=None):
+        self.matmul = QMatMul(weight)
+        self.bias = bias
+
+    @classmethod
+    def from_arc(cls, weight: QTensor, bias=None) -> "Linear":
+        return cls(weight, bias)
+
+    def forward(self, x, act: int = ACT_NONE, out_dtype=None, stream=None):
+        return self.matmul.forward(x, bias=self.bias, act=act, out_dtype=out_dtype, stream=stream)
+
+    __call__ = forward
