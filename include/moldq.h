@@ -86,6 +86,16 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
 int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
                            const void *dev_blocks, size_t nbytes, void *stream,
                            mq_qtensor **out);
+/* Quantize a dense f32 matrix already on the device, src[n, k] with row
+ * stride ld (elements), into a new device-resident GGUF weight of `dtype`.
+ * The blocks are byte-identical to ggml's reference quantizers
+ * (quantize_row_*_ref), which candle's k_quants port mirrors.  Replaces
+ * QTensor::quantize / quantize_onto (crates/mold-inference/src/flux/
+ * pipeline.rs:219-229, crates/mold-inference/src/flux/lora.rs:849).
+ * Runs on `stream` after work already queued there and returns when the
+ * blocks are in place (it uses and frees a temporary staging buffer). */
+int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld,
+                void *stream, mq_qtensor **out);
 /* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
  * Synchronous. */
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes);

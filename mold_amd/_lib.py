@@ -27,6 +27,7 @@ SIGNATURES = {
     "mq_ctx_reserve_scratch": (_int, [_vp, _sz]),
     "mq_qtensor_upload": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _pp]),
     "mq_qtensor_from_device": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _vp, _pp]),
+    "mq_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _vp, _pp]),
     "mq_qtensor_download": (_int, [_vp, _vp, _vp, _sz]),
     "mq_qtensor_free": (None, [_vp]),
     "mq_qtensor_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(_i64),

@@ -263,6 +263,36 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
   return MQ_OK;
 }
 
+int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld, void *stream,
+                mq_qtensor **out) {
+  if (!ctx || !out || !src) return fail(MQ_E_INVALID, "mq_quantize: NULL argument");
+  *out = nullptr;
+  if (!is_quant(dtype)) return fail(MQ_E_INVALID, "mq_quantize: dtype %d is not a GGUF block type", dtype);
+  if (n <= 0 || k <= 0 || ld < k)
+    return fail(MQ_E_INVALID, "mq_quantize: bad shape n=%lld k=%lld ld=%lld", (long long)n, (long long)k, (long long)ld);
+  const TypeInfo ti = type_info(dtype);
+  if (k % ti.bs != 0) return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", ti.name, ti.bs, (long long)k);
+  DeviceGuard g(ctx->device);
+  const size_t nbytes = gguf_row_bytes(dtype, k) * (size_t)n;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void *staging = nullptr;
+  hipError_t e = hipMalloc(&staging, nbytes);
+  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) staging failed: %s", nbytes, hipGetErrorString(e));
+  e = launch_quantize(dtype, src, ld, n, k, staging, s);
+  int rc = MQ_OK;
+  if (e != hipSuccess) rc = hip_fail(e, "quantize launch");
+  if (rc == MQ_OK) rc = mq_qtensor_from_device(ctx, dtype, n, k, staging, nbytes, stream, out);
+  const hipError_t se = hipStreamSynchronize(s);
+  (void)hipFree(staging);
+  if (rc != MQ_OK) return rc;
+  if (se != hipSuccess) {
+    mq_qtensor_free(*out);
+    *out = nullptr;
+    return hip_fail(se, "quantize synchronize");
+  }
+  return MQ_OK;
+}
+
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes) {
   if (!ctx || !w || !host_blocks) return fail(MQ_E_INVALID, "mq_qtensor_download: NULL argument");
   if (nbytes != w->gguf_bytes) return fail(MQ_E_INVALID, "download needs %zu bytes, got %zu", w->gguf_bytes, nbytes);

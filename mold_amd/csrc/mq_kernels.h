@@ -12,6 +12,9 @@ namespace mq {
 
 hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, bool inverse,
                          hipStream_t stream);
+// f32 [n, k] (row stride ld) -> raw GGUF blocks (n rows of k/bs blocks).
+hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, int64_t k, void *dst_raw,
+                           hipStream_t stream);
 hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
                           hipStream_t stream);
 // bf16 [m, k] (row stride ldx) -> f32 [m, k] contiguous, for the GEMV.

@@ -56,11 +56,20 @@ __device__ __forceinline__ void store8<float>(float *dst, const float v[8]) {
   reinterpret_cast<float4 *>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
+// Half outputs are the f32 dequantized value rounded once more to nearest
+// even.  pin() keeps that f32 value in a register: otherwise the backend fuses
+// the decoder's last multiply-add into the conversion (v_fma_mix*_f16), which
+// rounds the exact product-sum straight to f16 and can differ in the last bit.
+__device__ __forceinline__ float pin(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 template <>
 __device__ __forceinline__ void store8<__bf16>(__bf16 *dst, const float v[8]) {
   bf16x8 r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = (__bf16)v[i];
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)pin(v[i]);
   *reinterpret_cast<bf16x8 *>(dst) = r;
 }
 
@@ -68,7 +77,7 @@ template <>
 __device__ __forceinline__ void store8<_Float16>(_Float16 *dst, const float v[8]) {
   f16x8 r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = (_Float16)v[i];
+  for (int i = 0; i < 8; ++i) r[i] = (_Float16)pin(v[i]);
   *reinterpret_cast<f16x8 *>(dst) = r;
 }
 

@@ -140,6 +140,19 @@ class QTensor:
         return cls(device, h)
 
     @classmethod
+    def quantize(cls, device: Device, src, dtype: GgmlDType, stream=None) -> "QTensor":
+        """candle QTensor::quantize_onto: f32 [n, k] device tensor -> GGUF blocks
+        quantized on the GPU (ggml reference quantizer, byte-identical)."""
+        torch = _torch()
+        if src.dtype != torch.float32 or src.dim() != 2 or src.stride(1) != 1:
+            raise ValueError("QTensor.quantize needs a 2-D f32 device tensor with unit column stride")
+        n, k = src.shape
+        h = ctypes.c_void_p()
+        check(_lib.load().mq_quantize(device.handle, int(dtype), n, k, src.data_ptr(), src.stride(0),
+                                      _stream_ptr(stream), ctypes.byref(h)))
+        return cls(device, h)
+
+    @classmethod
     def from_device_blocks(cls, device: Device, dtype: GgmlDType, shape: Sequence[int], blocks_tensor,
                            stream=None) -> "QTensor":
         """Build from GGUF blocks already in device memory (a uint8 torch tensor)."""
@@ -212,7 +225,8 @@ class QMatMul:
         if x2.stride(1) != 1:
             x2 = x2.contiguous()
         m = x2.shape[0]
-        out_dtype = x.dtype if out_dtype is None else out_dtype
+        if out_dtype is None:
+            out_dtype = out.dtype if out is not None else x.dtype
         if out is None:
             out = torch.empty((m, n), dtype=out_dtype, device=x.device)
         else:

@@ -1,0 +1,430 @@
+"""GPU parity of libmoldq (HIP, gfx950) against the CPU oracle, through the C ABI.
+
+Bars:
+  * dequantized weights bit-exact with the GGUF formulas (oracle/ggml_oracle.c
+    restates ggml's dequantize_row_*; candle's QTensor::dequantize evaluates
+    the same formulas, called at crates/mold-inference/src/qwen_image/
+    quantized_transformer.rs:62-66);
+  * QMatMul::forward output within rel-L2 1e-2 of an f64-accumulated
+    dequantize-then-matmul (the GEMV, which accumulates in f32 from the exact
+    weights, is held to 1e-5);
+  * no NaN for finite inputs (the reference scrubs NaN from candle's CUDA
+    QMatMul, crates/mold-inference/src/flux2/quantized_transformer.rs:40-45);
+  * identical outputs on repeated calls (no races in the LDS pipeline).
+Full BASELINE shapes are checked on sampled rows plus size-independent
+properties (linearity, determinism, NaN-freedom).
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import mold_amd
+from mold_amd import GgmlDType, QMatMul, QTensor
+from mold_amd._lib import MoldqError
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-2   # BASELINE: rel-L2 <= 1e-2 vs f32 dequantize-then-matmul
+GEMV_TOL = 1e-5   # f32 accumulation of exact weights
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    return _t
+
+
+@pytest.fixture(scope="module")
+def dev(torch):
+    d = mold_amd.Device(0)
+    yield d
+    torch.cuda.synchronize()
+
+
+def _weights(t, n, k, seed, scale=0.02):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * scale).astype(np.float32)
+    return O.quantize(t, w)
+
+
+def _random_blocks(t, n, k, seed):
+    """Arbitrary bytes: every byte pattern is a valid GGUF block (f16 scales may be
+    subnormal, Inf or NaN)."""
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, 256, size=(n, O.row_bytes(t, k)), dtype=np.uint8)
+
+
+def _bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    na, nb = np.isnan(a), np.isnan(b)
+    if not np.array_equal(na, nb):
+        return False
+    return np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb])
+
+
+TYPES = [GgmlDType(t) for t in O.WEIGHT_TYPES]
+IDS = [t.name for t in TYPES]
+
+
+# ------------------------------------------------------------- upload / dequant
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+def test_upload_download_byte_identical(dev, t):
+    n, k = 131, 2 * 256
+    _say(f"upload/download {t.name} [{n},{k}]")
+    blocks = _random_blocks(int(t), n, k, 1)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    assert qt.dtype() == t and qt.shape == (n, k)
+    assert qt.storage_size_in_bytes() == blocks.nbytes
+    assert np.array_equal(qt.data(), blocks.reshape(-1))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+@pytest.mark.parametrize("shape", [(1, 256), (64, 512), (130, 768), (257, 256)], ids=str)
+def test_dequantize_bit_exact_quantized_weights(dev, torch, t, shape):
+    n, k = shape
+    _say(f"dequant {t.name} {shape}")
+    blocks = _weights(int(t), n, k, seed=n + k)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    got = qt.dequantize().cpu().numpy()
+    torch.cuda.synchronize()
+    assert _bits_equal(got, O.dequantize(int(t), blocks, n, k))
+
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+def test_dequantize_bit_exact_random_bytes(dev, torch, t):
+    n, k = 67, 512
+    _say(f"dequant random bytes {t.name}")
+    blocks = _random_blocks(int(t), n, k, 7)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    got = qt.dequantize().cpu().numpy()
+    assert _bits_equal(got, O.dequantize(int(t), blocks, n, k))
+
+
+@pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q8_0, GgmlDType.Q6_K, GgmlDType.Q3_K], ids=lambda t: t.name)
+def test_dequantize_half_outputs_round_nearest_even(dev, torch, t):
+    n, k = 96, 512
+    _say(f"dequant f16/bf16 {t.name}")
+    blocks = _weights(int(t), n, k, seed=3, scale=1.0)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    exact = torch.from_numpy(O.dequantize(int(t), blocks, n, k))
+    for dt in (torch.bfloat16, torch.float16):
+        got = qt.dequantize(dtype=dt).cpu()
+        assert torch.equal(got.view(torch.int16), exact.to(dt).view(torch.int16)), dt
+    # arbitrary blocks: scales of every magnitude (double rounding would show here)
+    blocks = _random_blocks(int(t), n, k, 8)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    exact = torch.from_numpy(O.dequantize(int(t), blocks, n, k))
+    nan = torch.isnan(exact)
+    for dt in (torch.bfloat16, torch.float16):
+        got = qt.dequantize(dtype=dt).cpu()
+        assert torch.equal(torch.isnan(got), nan), dt
+        assert torch.equal(got[~nan].view(torch.int16), exact[~nan].to(dt).view(torch.int16)), dt
+
+
+# --------------------------------------------------------------------- GEMV
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+def test_gemv_matches_f64_oracle(dev, torch, t, m):
+    n, k = 200, 1024
+    _say(f"gemv {t.name} m={m}")
+    blocks = _weights(int(t), n, k, seed=m)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    rng = np.random.default_rng(100 + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    assert O.rel_l2(y, ref) <= GEMV_TOL
+    assert np.isfinite(y).all()
+
+
+def test_gemv_bias_gelu_strides_bf16(dev, torch):
+    t, n, k, m = GgmlDType.Q4_K, 300, 768, 2
+    _say("gemv bias/gelu/strides/bf16")
+    blocks = _weights(int(t), n, k, seed=11)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    ref = O.matmul_f64(int(t), x, blocks, n, k) + b
+    gelu = 0.5 * ref * (1 + np.tanh(np.sqrt(2 / np.pi) * (ref + 0.044715 * ref ** 3)))
+    bias = torch.from_numpy(b).cuda()
+    # strided x: view into a wider buffer
+    xw = torch.zeros((m, k + 64), dtype=torch.float32, device="cuda")
+    xw[:, :k] = torch.from_numpy(x).cuda()
+    lin = mold_amd.Linear(qt, bias)
+    y = lin.forward(xw[:, :k], act=mold_amd.ACT_GELU_TANH).cpu().numpy()
+    assert O.rel_l2(y, gelu) <= GEMV_TOL
+    # bf16 in / bf16 out
+    xb = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    ref_b = O.matmul_f64(int(t), xb.float().cpu().numpy(), blocks, n, k) + b
+    yb = lin.forward(xb).float().cpu().numpy()
+    assert O.rel_l2(yb, ref_b) <= 1e-2
+
+
+def test_gemv_ksplit_large_k(dev, torch):
+    # few row tiles, long K: the launcher splits K across workgroups
+    t, n, k, m = GgmlDType.Q4_K, 64, 256 * 48, 4
+    _say("gemv k-split")
+    blocks = _weights(int(t), n, k, seed=5)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = np.random.default_rng(6).standard_normal((m, k)).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert O.rel_l2(y, O.matmul_f64(int(t), x, blocks, n, k)) <= GEMV_TOL
+
+
+# --------------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+@pytest.mark.parametrize("mnk", [(9, 64, 256), (300, 200, 512), (513, 320, 768)], ids=str)
+def test_gemm_matches_f64_oracle(dev, torch, t, mnk):
+    m, n, k = mnk
+    _say(f"gemm {t.name} {mnk}")
+    blocks = _weights(int(t), n, k, seed=m + n)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    err = O.rel_l2(y, ref)
+    assert err <= GEMM_TOL, err
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("t", [GgmlDType.Q4_0, GgmlDType.Q8_0, GgmlDType.Q5_1], ids=lambda t: t.name)
+def test_gemm_k_not_multiple_of_64(dev, torch, t):
+    # 32-element blocks allow k = 32 * odd: the last K step is half padding
+    m, n, k = 100, 96, 32 * 13
+    _say(f"gemm ragged k {t.name}")
+    blocks = _weights(int(t), n, k, seed=2)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = np.random.default_rng(4).standard_normal((m, k)).astype(np.float32)
+    for xdt in (torch.float32, torch.bfloat16):
+        xt = torch.from_numpy(x).cuda().to(xdt)
+        y = QMatMul(qt).forward(xt).float().cpu().numpy()
+        ref = O.matmul_f64(int(t), xt.float().cpu().numpy(), blocks, n, k)
+        assert O.rel_l2(y, ref) <= GEMM_TOL
+
+
+def test_gemm_bias_gelu_bf16_and_strides(dev, torch):
+    t, m, n, k = GgmlDType.Q4_K, 260, 384, 1024
+    _say("gemm bias/gelu/bf16/strides")
+    blocks = _weights(int(t), n, k, seed=21)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    ref = O.matmul_f64(int(t), x, blocks, n, k) + b
+    gelu = 0.5 * ref * (1 + np.tanh(np.sqrt(2 / np.pi) * (ref + 0.044715 * ref ** 3)))
+    lin = mold_amd.Linear(qt, torch.from_numpy(b).cuda())
+    xw = torch.zeros((m, k + 128), dtype=torch.float32, device="cuda")
+    xw[:, :k] = torch.from_numpy(x).cuda()
+    y = lin.forward(xw[:, :k], act=mold_amd.ACT_GELU_TANH).cpu().numpy()
+    assert O.rel_l2(y, gelu) <= GEMM_TOL
+    # bf16 activations read in place (k % 64 == 0, aligned rows), bf16 output
+    xb = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    yb = lin.forward(xb, out_dtype=torch.bfloat16)
+    assert yb.dtype == torch.bfloat16
+    ref_b = O.matmul_f64(int(t), xb.float().cpu().numpy(), blocks, n, k) + b
+    assert O.rel_l2(yb.float().cpu().numpy(), ref_b) <= GEMM_TOL
+    # output with a row stride: write into a slice of a wider buffer
+    out = torch.full((m, n + 32), 7.0, dtype=torch.float32, device="cuda")
+    ys = lin.matmul.forward(torch.from_numpy(x).cuda(), bias=lin.bias, out=out[:, :n])
+    assert O.rel_l2(ys.cpu().numpy(), ref) <= GEMM_TOL
+    assert torch.all(out[:, n:] == 7.0)
+
+
+def test_gemm_and_gemv_deterministic(dev, torch):
+    t, n, k = GgmlDType.Q4_K, 512, 1536
+    _say("determinism")
+    qt = QTensor.from_blocks(dev, t, (n, k), _weights(int(t), n, k, seed=31))
+    mm = QMatMul(qt)
+    for m in (1, 4, 700):
+        x = torch.randn((m, k), generator=torch.Generator().manual_seed(m)).cuda()
+        a = mm.forward(x).clone()
+        b = mm.forward(x).clone()
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), m
+
+
+def test_gpu_within_bar_of_candle_cpu_algorithm(dev, torch):
+    # candle's CPU QMatMul quantizes x to Q8_0/Q8_1/Q8_K first; both it and the
+    # GPU path must sit inside the 1e-2 envelope of the exact reference.
+    _say("gpu vs candle cpu algorithm")
+    m, n, k = 64, 256, 1024
+    x = np.random.default_rng(41).standard_normal((m, k)).astype(np.float32)
+    for t in TYPES:
+        blocks = _weights(int(t), n, k, seed=42)
+        qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+        y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+        cand = O.matmul_candle(int(t), x, blocks, n, k)
+        assert O.rel_l2(y, cand) <= 2 * GEMM_TOL, t.name
+        assert O.rel_l2(cand, O.matmul_f64(int(t), x, blocks, n, k)) <= GEMM_TOL, t.name
+
+
+# --------------------------------------------------------- errors and edges
+
+def test_errors_are_reported_not_raised_as_crashes(dev, torch):
+    _say("error paths")
+    lib = mold_amd.load()
+    h = ctypes.c_void_p()
+    blocks = _weights(int(GgmlDType.Q4_K), 4, 256, seed=1)
+    # k not a multiple of the block size
+    assert lib.mq_qtensor_upload(dev.handle, int(GgmlDType.Q4_K), 4, 255, blocks.ctypes.data, blocks.nbytes,
+                                 ctypes.byref(h)) == mold_amd._lib.MQ_E_INVALID
+    # byte count mismatch
+    assert lib.mq_qtensor_upload(dev.handle, int(GgmlDType.Q4_K), 4, 256, blocks.ctypes.data, blocks.nbytes - 1,
+                                 ctypes.byref(h)) == mold_amd._lib.MQ_E_INVALID
+    qt = QTensor.from_blocks(dev, GgmlDType.Q4_K, (4, 256), blocks)
+    with pytest.raises(ValueError):
+        QMatMul(qt).forward(torch.zeros((3, 128), device="cuda"))
+    with pytest.raises(MoldqError):
+        QMatMul(qt).forward(torch.zeros((3, 256), device="cuda", dtype=torch.float16))
+    # m = 0 is a no-op
+    y = QMatMul(qt).forward(torch.zeros((0, 256), device="cuda"))
+    assert tuple(y.shape) == (0, 4)
+
+
+def test_zero_weights_and_single_block(dev, torch):
+    _say("zero / single-block weights")
+    t, n, k = GgmlDType.Q4_K, 70, 512
+    blocks = np.zeros((n, O.row_bytes(int(t), k)), np.uint8)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = torch.randn((300, k), generator=torch.Generator().manual_seed(0)).cuda()
+    assert torch.count_nonzero(QMatMul(qt).forward(x)) == 0
+    assert torch.count_nonzero(QMatMul(qt).forward(x[:2])) == 0
+    # one non-zero row: output column equals x . row
+    w = np.zeros((n, k), np.float32)
+    w[5] = np.random.default_rng(1).standard_normal(k) * 0.02
+    blocks = O.quantize(int(t), w)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    y = QMatMul(qt).forward(x).cpu().numpy()
+    ref = O.matmul_f64(int(t), x.cpu().numpy(), blocks, n, k)
+    assert np.count_nonzero(y[:, np.arange(n) != 5]) == 0
+    assert O.rel_l2(y[:, 5], ref[:, 5]) <= GEMM_TOL
+
+
+def test_gguf_file_to_device(dev, torch, tmp_path):
+    _say("gguf load")
+    from mold_amd import gguf
+    tensors = []
+    for i, t in enumerate((GgmlDType.Q4_K, GgmlDType.Q8_0, GgmlDType.Q2_K)):
+        n, k = 65 + i, 512
+        tensors.append((f"double_blocks.{i}.img_mlp.0.weight", t, (n, k), _weights(int(t), n, k, seed=i)))
+    p = str(tmp_path / "w.gguf")
+    gguf.write(p, tensors)
+    c = gguf.Content.read(p)
+    for name, t, (n, k), blocks in tensors:
+        qt = c.tensor(name, dev)
+        assert qt.dtype() == t and qt.shape == (n, k)
+        assert np.array_equal(qt.data(), blocks.reshape(-1))
+        assert _bits_equal(qt.dequantize().cpu().numpy(), O.dequantize(int(t), blocks, n, k))
+    c.close()
+
+
+def test_arena_residency(torch):
+    _say("arena")
+    d = mold_amd.Device(0)
+    d.reserve_arena(64 << 20)
+    ws = []
+    for i, t in enumerate(TYPES):
+        blocks = _weights(int(t), 128, 512, seed=i)
+        ws.append((t, blocks, QTensor.from_blocks(d, t, (128, 512), blocks)))
+    for t, blocks, qt in ws:
+        assert np.array_equal(qt.data(), blocks.reshape(-1)), t.name
+    del ws
+    d.close()
+
+
+# ----------------------------------------------------- BASELINE full shapes
+
+def _sampled_rows_check(dev, torch, t, m, n, k, seed, rows=24):
+    blocks = _weights(int(t), n, k, seed=seed)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    mm = QMatMul(qt)
+    y = mm.forward(x)
+    assert not torch.isnan(y).any().item()
+    idx = np.sort(np.random.default_rng(seed).choice(m, size=rows, replace=False))
+    idx[-1] = m - 1
+    xs = x[torch.from_numpy(idx).cuda()].cpu().numpy()
+    ref = O.matmul_f64(int(t), xs, blocks, n, k)
+    err = O.rel_l2(y[torch.from_numpy(idx).cuda()].cpu().numpy(), ref)
+    assert err <= GEMM_TOL, err
+    # linearity: W(x1 + x2) = W x1 + W x2 (within bf16 staging error)
+    x2 = torch.randn((m, k), device="cuda", generator=g)
+    lin = (mm.forward(x + x2) - y - mm.forward(x2)).norm() / y.norm()
+    assert lin.item() <= 2 * GEMM_TOL
+    return err
+
+
+def test_full_flux_single_block_linear1_q4k(dev, torch):
+    _say("full shape Q4_K 4608x3072->21504")
+    _sampled_rows_check(dev, torch, GgmlDType.Q4_K, 4608, 21504, 3072, seed=4)
+
+
+def test_full_config1_q8_0_out_proj(dev, torch):
+    _say("full shape Q8_0 4608x3072->3072")
+    _sampled_rows_check(dev, torch, GgmlDType.Q8_0, 4608, 3072, 3072, seed=1)
+
+
+@pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q4_0, GgmlDType.Q6_K], ids=lambda t: t.name)
+def test_full_config3_mlp_fc2(dev, torch, t):
+    _say(f"full shape {t.name} 4608x12288->3072")
+    _sampled_rows_check(dev, torch, t, 4608, 3072, 12288, seed=3)
+
+
+@pytest.mark.parametrize("n", [18432, 9216])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_full_config2_modulation_gemv(dev, torch, n, m):
+    _say(f"full shape Q4_K GEMV m={m} 3072->{n}")
+    t, k = GgmlDType.Q4_K, 3072
+    blocks = _weights(int(t), n, k, seed=2)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert O.rel_l2(y, O.matmul_f64(int(t), x, blocks, n, k)) <= GEMV_TOL
+
+
+# ------------------------------------------------------------- quantizer
+
+def _quant_inputs(k, seed):
+    rng = np.random.default_rng(seed)
+    rows = [
+        rng.standard_normal(k) * 0.02,                      # BASELINE weight law
+        rng.standard_normal(k),
+        np.zeros(k),                                        # all-zero blocks
+        np.full(k, 0.37),                                   # constant (max == min)
+        np.where(rng.random(k) < 0.1, rng.standard_normal(k) * 50, rng.standard_normal(k) * 1e-3),  # outliers
+        rng.standard_normal(k) * 1e-20,                     # below GROUP_MAX_EPS
+        np.abs(rng.standard_normal(k)),                     # one-signed (min > 0)
+        -np.abs(rng.standard_normal(k)) * 3,
+    ]
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+def test_gpu_quantizer_byte_identical_to_reference(dev, torch, t):
+    _say(f"quantize {t.name}")
+    k = 512
+    x = _quant_inputs(k, seed=int(t))
+    xt = torch.from_numpy(x).cuda()
+    qt = QTensor.quantize(dev, xt, t)
+    got = qt.data().reshape(x.shape[0], -1)
+    ref = O.quantize(int(t), x)
+    bad = [i for i in range(x.shape[0]) if not np.array_equal(got[i], ref[i])]
+    assert not bad, f"rows differ: {bad}"
+    # strided source (row stride > k) gives the same blocks
+    wide = torch.zeros((x.shape[0], k + 64), device="cuda")
+    wide[:, :k] = xt
+    qs = QTensor.quantize(dev, wide[:, :k], t)
+    assert np.array_equal(qs.data(), ref.reshape(-1))
