@@ -175,24 +175,44 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fast path (k % 256 == 0): per-type B decoders from mq_bfrag.h.
-//   * each lane keeps the packed bytes of its two weight rows for the current
-//     K unit (256 weights; 128 for Q8_0) and loads the next unit's while the
-//     current one is consumed, so weight loads have a whole unit of MFMA work
-//     to land;
-//   * scales are unpacked once per unit, nibbles are masked in place and
-//     turned into f32 with v_cvt_f32_ubyte, one fma applies scale and min,
-//     v_cvt_pk_bf16_f32 packs the fragment — about 2.75 VALU ops per weight,
-//     each weight decoded once per 256-row block tile;
-//   * the activation tile goes global -> VGPR -> LDS one K step ahead, LDS
-//     double buffered, XOR-swizzled, one barrier per step.
+// Fast path (k % 256 == 0): 256 x 256 block tile, 8 waves (two per SIMD, so
+// one wave's dequant VALU work co-issues with the other's MFMAs), K step 64.
+//   * A (bf16 activations): 3-slot LDS ring filled by direct global->LDS
+//     loads (global_load_lds_dwordx4) two K steps ahead;
+//   * B (weights): wave w decodes rows 32w..32w+31 of the block's 256 weight
+//     rows for the NEXT K step (per-type decoders, mq_bfrag.h) and writes the
+//     bf16 tile to a 2-slot LDS ring, so every weight is decoded once per
+//     block tile; its packed bytes are reloaded into registers for the next
+//     unit one step after their last use;
+//   * MFMA: wave (wm = w&1, wn = w>>1) owns output rows 128wm.. and columns
+//     64wn..: 4 x 2 tiles of v_mfma_f32_32x32x16_bf16 per 16-K slice;
+//   * LDS rows are 128 B (64 bf16); 16-byte chunk c of row r sits in slot
+//     c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128 quarter (16
+//     consecutive rows) cover all 64 banks;
+//   * one barrier per step: s_waitcnt vmcnt(4) (the only younger memory ops
+//     are this step's four A loads) lgkmcnt(0), then s_barrier.
+constexpr int kAStages = 3;
+constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
+constexpr int kFastThreads = 512;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void step_barrier(bool more) {
+  if (more)
+    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ int lds_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+
 template <int TYPE, typename OUT>
-__global__ __launch_bounds__(kGemmThreads, 1) void gemm_fast_kernel(
+__global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
     OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act, int tiles_m, int tiles_n) {
   using TT = bfrag::T<TYPE>;
   constexpr int kSteps = TT::kUnitK / kBK;
-  __shared__ uint4 lds[2][kBM * kBK / 8];
+  __shared__ uint4 lds_a[kAStages][kBM * kBK / 8];
+  __shared__ uint4 lds_b[2][kBN * kBK / 8];
 
   const int total = tiles_m * tiles_n;
   const int bid = blockIdx.x;
@@ -204,112 +224,174 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_fast_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int phase = (wave >> 2) & 1;
+  const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane touches
   const int64_t m0 = (int64_t)mt * kBM;
-  const int64_t wt_raw = (int64_t)nt * (kBN / kRowTile) + wave;
-  const int64_t wt = wt_raw < ntiles_w ? wt_raw : ntiles_w - 1;  // keep reads in bounds
   const int64_t units = k / TT::kUnitK;
+  const int64_t ksteps = units * kSteps;
 
-  f32x16 acc[8][2];
+  // decoder role: weight tile nt*4 + wave/2, row (wave&1)*32 + l32 of it
+  const int64_t dt_raw = (int64_t)nt * (kBN / kRowTile) + (wave >> 1);
+  const int64_t dt = dt_raw < ntiles_w ? dt_raw : ntiles_w - 1;  // keep reads in bounds
+  const int drow = (wave & 1) * 32 + l32;
+  const int brow = 32 * wave + l32;  // its row in the LDS B tile
+
+  f32x16 acc[4][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // A staging: thread -> chunk ac (8 bf16) of rows ar + 32 i; rows past m
-  // read row m-1 (finite, never stored).
-  const int ac = tid & 7, ar = tid >> 3;
-  const __bf16 *arow[8];
+  // A DMA: load i (0..3) of wave w fills LDS rows 8(4w+i)..+7 (1 KiB); lane
+  // j fetches row 8(4w+i) + j/8, logical chunk (j&7) ^ ((row >> 1) & 7).
+  // Rows past m read row m-1 (finite, never stored).
+  int64_t aoff[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int64_t row = m0 + ar + 32 * i;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * (4 * wave + i) + (lane >> 3);
+    int64_t row = m0 + r;
     row = row < m ? row : m - 1;
-    arow[i] = a + row * lda + ac * 8;
+    aoff[i] = row * lda + (((lane & 7) ^ ((r >> 1) & 7)) * 8);
   }
-  uint4 a0, a1, a2, a3, a4, a5, a6, a7;
-#define MQ_LOAD_A(ks)                                                           \
-  do {                                                                          \
-    const int64_t _o = (ks) * kBK;                                              \
-    a0 = *reinterpret_cast<const uint4 *>(arow[0] + _o);                        \
-    a1 = *reinterpret_cast<const uint4 *>(arow[1] + _o);                        \
-    a2 = *reinterpret_cast<const uint4 *>(arow[2] + _o);                        \
-    a3 = *reinterpret_cast<const uint4 *>(arow[3] + _o);                        \
-    a4 = *reinterpret_cast<const uint4 *>(arow[4] + _o);                        \
-    a5 = *reinterpret_cast<const uint4 *>(arow[5] + _o);                        \
-    a6 = *reinterpret_cast<const uint4 *>(arow[6] + _o);                        \
-    a7 = *reinterpret_cast<const uint4 *>(arow[7] + _o);                        \
-  } while (0)
-#define MQ_STORE_A(buf)                                                         \
-  do {                                                                          \
-    uint4 *_l = lds[buf];                                                       \
-    _l[(ar + 0) * 8 + (ac ^ ((ar + 0) & 7))] = a0;                              \
-    _l[(ar + 32) * 8 + (ac ^ ((ar + 32) & 7))] = a1;                            \
-    _l[(ar + 64) * 8 + (ac ^ ((ar + 64) & 7))] = a2;                            \
-    _l[(ar + 96) * 8 + (ac ^ ((ar + 96) & 7))] = a3;                            \
-    _l[(ar + 128) * 8 + (ac ^ ((ar + 128) & 7))] = a4;                          \
-    _l[(ar + 160) * 8 + (ac ^ ((ar + 160) & 7))] = a5;                          \
-    _l[(ar + 192) * 8 + (ac ^ ((ar + 192) & 7))] = a6;                          \
-    _l[(ar + 224) * 8 + (ac ^ ((ar + 224) & 7))] = a7;                          \
-  } while (0)
+  auto dma_a = [&](int64_t ks) {
+    uint4 *dst = &lds_a[ks % kAStages][(32 * wave) * 8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(static_cast<const void *>(a + aoff[i] + ks * kBK),
+                                       (lds_void_t *)(dst + 64 * i), 16, 0, 0);
+  };
 
-  typename TT::Raw cur[2], nxt[2];
-  TT::load(cur[0], w, wt, l32, 0, h);
-  TT::load(cur[1], w, wt, l32 + 32, 0, h);
-  MQ_LOAD_A(0);
-  MQ_STORE_A(0);
-  __syncthreads();
+  typename TT::Raw raw;
+  typename TT::Sc sc;
+  auto decode_to = [&]<int G>(int buf) {
+    uint4 *dst = lds_b[buf];
+    static_for<4>([&]<int S>() {
+      const bf16x8 f = TT::template frag<G, S>(raw, sc);
+      uint4 q;
+      __builtin_memcpy(&q, &f, 16);
+      dst[brow * 8 + (TT::chunk(S, h) ^ swz)] = q;
+    });
+  };
+
+  // prologue: unit 0's weight bytes, A(0), A(1); decode step 0
+  TT::load_prep(raw, w, dt, drow, 0, h);
+  static_for<kSteps>([&]<int G>() { TT::template reload<G>(raw, w, dt, drow, 0, h); });
+  dma_a(0);
+  if (ksteps > 1) dma_a(1);
+  if (ksteps > 1)
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  TT::prep(raw, sc, h);
+  decode_to.template operator()<0>(0);
+  step_barrier(ksteps > 1);
 
   for (int64_t u = 0; u < units; ++u) {
-    typename TT::Sc sc[2];
-    TT::prep(cur[0], sc[0], h);
-    TT::prep(cur[1], sc[1], h);
+    const bool next_unit = u + 1 < units;
     static_for<kSteps>([&]<int G>() {
       const int64_t ks = u * kSteps + G;
-      constexpr int buf = G & 1;
-      const bool more = ks + 1 < units * kSteps;
-      if (more) MQ_LOAD_A(ks + 1);
-      if constexpr (G == 0) {
-        if (u + 1 < units) {
-          TT::load(nxt[0], w, wt, l32, u + 1, h);
-          TT::load(nxt[1], w, wt, l32 + 32, u + 1, h);
-        }
+      // the pieces decoded last iteration (step G of unit u) are free: fetch
+      // unit u+1's; unit u's scales were unpacked last iteration too.
+      if (next_unit) {
+        TT::template reload<G>(raw, w, dt, drow, u + 1, h);
+        if constexpr (G == 0) TT::load_prep(raw, w, dt, drow, u + 1, h);
       }
-      bf16x8 bfr[2][4];
-      TT::template decode<G>(cur[0], sc[0], bfr[0]);
-      TT::template decode<G>(cur[1], sc[1], bfr[1]);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int chunk = TT::chunk(s, h);
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-          const int row = mb * 32 + l32;
-          const uint4 raw = lds[buf][row * 8 + (chunk ^ (row & 7))];
-          bf16x8 afrag;
-          __builtin_memcpy(&afrag, &raw, 16);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb)
-            acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(afrag, bfr[nb][s], acc[mb][nb], 0, 0, 0);
+      const bool more = ks + 2 < ksteps;
+      if (more) dma_a(ks + 2);
+
+      // decode the next step's weights into the other B slot
+      auto decode_next = [&]() {
+        if constexpr (G + 1 < kSteps) {
+          decode_to.template operator()<G + 1>((int)((ks + 1) & 1));
+        } else {
+          if (next_unit) {
+            TT::prep(raw, sc, h);
+            decode_to.template operator()<0>((int)((ks + 1) & 1));
+          }
         }
+      };
+      auto mfma_step = [&]() {
+        // Every fragment row this lane reads has (row >> 1) & 7 == swz, so the
+        // slot of slice S is fixed per lane and the 32-row tile offsets are
+        // immediates: one address register per slice.
+        const char *abase = reinterpret_cast<const char *>(lds_a[ks % kAStages]) + (wm * 128 + l32) * 128;
+        const char *bbase = reinterpret_cast<const char *>(lds_b[ks & 1]) + (wn * 64 + l32) * 128;
+        bf16x8 fr[2][6];  // [slot][B nb=0,1 | A mb=0..3]
+        auto read_frags = [&](bf16x8 *dst, int S) {
+          const int off = (TT::chunk(S, h) ^ swz) * 16;
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) dst[nb] = *reinterpret_cast<const bf16x8 *>(bbase + off + nb * 4096);
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) dst[2 + mb] = *reinterpret_cast<const bf16x8 *>(abase + off + mb * 4096);
+        };
+        read_frags(fr[0], 0);
+        static_for<4>([&]<int S>() {
+          if constexpr (S < 3) read_frags(fr[(S + 1) & 1], S + 1);
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+              acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[S & 1][2 + mb], fr[S & 1][nb], acc[mb][nb], 0,
+                                                                    0, 0);
+          // interleave: the next slice's six fragment reads between this
+          // slice's eight MFMAs
+          if constexpr (S < 3) {
+            static_for<6>([&]<int I>() {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+          } else {
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+          }
+        });
+      };
+      // The two waves sharing a SIMD (w and w+4) run the step's halves in
+      // opposite order, so one decodes (VALU) while the other runs MFMAs.
+      if (phase) {
+        decode_next();
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step();
+      } else {
+        mfma_step();
+        __builtin_amdgcn_sched_barrier(0);
+        decode_next();
       }
-      if (more) MQ_STORE_A(buf ^ 1);
-      __syncthreads();
+      step_barrier(more);
     });
-    cur[0] = nxt[0];
-    cur[1] = nxt[1];
   }
 
-  if (wt_raw >= ntiles_w) return;
+  const int64_t wt_out = (int64_t)nt * (kBN / kRowTile) + wn;
+  if (wt_out >= ntiles_w) return;
+  const int64_t row0 = m0 + wm * 128 + 4 * h;
+  const int64_t col0 = wt_out * kRowTile + l32;
+  if (m0 + kBM <= m && wt_out * kRowTile + kRowTile <= n && act == MQ_ACT_NONE_) {
+    // full tile, no activation: unchecked stores
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float bv = bias ? bias[col0 + nb * 32] : 0.f;
+      OUT *yc = y + row0 * ldy + col0 + nb * 32;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][nb][e] + bv);
+    }
+    return;
+  }
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const int64_t col = wt_raw * kRowTile + nb * 32 + l32;
+    const int64_t col = col0 + nb * 32;
     if (col >= n) continue;
     const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
+    for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + mb * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
         if (row < m) store_out<OUT>(y + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act));
       }
     }
@@ -327,10 +409,10 @@ hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t n
   bool ok = dispatch_type(type, [&]<int T>() {
     if (fast) {
       if (y_type == F32)
-        hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k,
+        hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
                            ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
       else
-        hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k,
+        hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
                            ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
       return;
     }
