@@ -374,7 +374,7 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
       ldxf = k;
     }
     hipError_t e = launch_gemv(w->dtype, wv, n, k, xf, m, ldxf, y, y_dtype, ldy, bias, act,
-                               static_cast<float *>(ctx->scratch), s);
+                               static_cast<float *>(ctx->scratch), ctx->cu_count, s);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return MQ_OK;
   }

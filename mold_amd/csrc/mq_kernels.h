@@ -24,13 +24,14 @@ hipError_t launch_stage_bf16(const void *x, int x_type, int64_t m, int64_t k, in
                              int64_t kp, hipStream_t stream);
 
 // Skinny-M GEMV (m <= kGemvMaxM).  `partial` is scratch of
-// ksplit*m*ntiles*64 floats when the launcher decides to split K (it returns
-// the bytes it needs through gemv_scratch_bytes first).
+// ksplit*m*ntiles*64 floats when the launcher decides to split K across
+// workgroups (gemv_scratch_bytes returns what it needs; 0 for the Q4_K path,
+// which adds its K-split partials inside the workgroup).
 constexpr int kGemvMaxM = 8;
 size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const float *x, int64_t m,
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
-                       float *partial, hipStream_t stream);
+                       float *partial, int cus, hipStream_t stream);
 
 // Fused dequant -> LDS -> bf16 MFMA GEMM.  a is bf16 [m, lda] with lda a
 // multiple of 64 covering ceil(k/64)*64 zero-padded columns.
