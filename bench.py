@@ -14,7 +14,9 @@ Also reported on the same JSON line:
   * "gemv": the skinny-M Q4_K modulation GEMVs (config 2, M in {1, 2, 4},
     N in {18432, 9216}), rotating through > 256 MB of distinct weight copies
     so reads miss the Infinity Cache, in GB/s of algorithmic bytes against
-    the 8 TB/s HBM peak;
+    the 8 TB/s HBM peak.  The rotation is captured once in a HIP graph and
+    replayed, so the figure is the kernels' own rate, not Python's launch
+    rate;
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
     oracle/ and timed on a bounded row sample of the same workload on this
@@ -23,13 +25,20 @@ Also reported on the same JSON line:
 Weights are N(0, 0.02^2) quantized to GGUF blocks on the GPU by libmoldq's
 quantizer when available; activations are N(0, 1) from torch's seeded
 generator.  Everything is resident in HBM before the timed region.
+HBM traffic per GEMM launch ("roofline.traffic") comes from the committed
+rocprofv3 counter summary profiles/gemm_q4k_linear1_traffic.md (FETCH_SIZE and
+WRITE_SIZE of `python3 bench.py --pmc-pass`, each scaled by what the counter
+reads for a plain copy of known size in the same run); null if absent.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv]
+       python bench.py --pmc-pass     (few launches of each kernel, for counters)
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -39,6 +48,8 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+GEMM_KERNEL = "mq::gemm_fast_kernel<12, float>"   # Q4_K weights, f32 output
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q4k_linear1_traffic.md")
 
 
 def log(msg):
@@ -123,22 +134,71 @@ def bench_gemv(dev, args):
             g = torch.Generator(device="cuda").manual_seed(m)
             x = torch.randn((m, k), device="cuda", generator=g)
             y = torch.empty((m, n), device="cuda")
-            for mm in mms:
-                mm.forward(x, out=y)
-            torch.cuda.synchronize()
-            iters = max(4, args.steps // 2)
 
             def run():
                 for mm in mms:
                     mm.forward(x, out=y)
-            ms = time_events(run, iters) / copies
+            run()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run()
+            graph.replay()
+            torch.cuda.synchronize()
+            iters = max(10, args.steps)
+            ms = time_events(graph.replay, iters) / copies
             nbytes = wbytes + 4 * m * k + 4 * m * n
-            out.append({"m": m, "n": n, "k": k, "us": ms * 1e3, "bytes": nbytes,
-                        "gbs": nbytes / (ms * 1e-3) / 1e9, "frac": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS})
+            out.append({"m": m, "n": n, "k": k, "us": round(ms * 1e3, 3), "bytes": nbytes,
+                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
             log(f"  m={m} n={n}: {ms*1e3:.2f} us  {out[-1]['gbs']:.0f} GB/s")
+            del graph
         del mms, qts
         torch.cuda.empty_cache()
     return out
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            text = f.read()
+    except OSError:
+        return None
+    mt = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(mt.group(1)) if mt else None
+
+
+def pmc_pass(dev, args):
+    """A short run for rocprofv3 counter passes: a 256 MiB device copy (the
+    calibration kernel, bytes known exactly), then the GEMM kernel alone
+    (bf16 activations, f32 out) and the M=1 3072->18432 Q4_K GEMV."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    nbytes = 256 << 20
+    a = torch.empty(nbytes // 4, device="cuda").normal_()
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copy calibration: {nbytes} bytes read + {nbytes} written per launch")
+    m, n, k = 4608, 21504, 3072
+    mm = mold_amd.QMatMul(make_weight(dev, GgmlDType.Q4_K, n, k, seed=4))
+    g = torch.Generator(device="cuda").manual_seed(40)
+    xb = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty((m, n), device="cuda")
+    for _ in range(3):
+        mm.forward(xb, out=y)
+    torch.cuda.synchronize()
+    log("GEMM launches done")
+    gv = mold_amd.QMatMul(make_weight(dev, GgmlDType.Q4_K, 18432, k, seed=200))
+    x1 = torch.randn((1, k), device="cuda")
+    y1 = torch.empty((1, 18432), device="cuda")
+    for _ in range(3):
+        gv.forward(x1, out=y1)
+    torch.cuda.synchronize()
+    log("GEMV launches done")
 
 
 def cpu_baseline(blocks, x, n, k, budget_s=12.0):
@@ -167,6 +227,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--pmc-pass", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -177,6 +238,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     mold_amd.load()
     dev = mold_amd.Device(0)
+    if args.pmc_pass:
+        pmc_pass(dev, args)
+        return
     gemm, blocks, x = bench_gemm(dev, args)
     log(f"GEMM: {gemm['ms_per_step']:.3f} ms/step {gemm['tflops']:.1f} TFLOP/s; kernel {gemm['kernel_ms']:.3f} ms "
         f"{gemm['kernel_tflops']:.1f} TFLOP/s")
@@ -203,8 +267,9 @@ def main():
                    "weight": "Q4_K", "x": "f32", "y": "f32"},
         "roofline": {"bound": "mfma", "achieved": round(gemm["kernel_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm["kernel_tflops"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "kernel": "gemm_kernel<Q4_K,float>",
-                     "kernel_ms": round(gemm["kernel_ms"], 4)},
+                     "traffic": read_traffic(), "kernel": GEMM_KERNEL,
+                     "kernel_ms": round(gemm["kernel_ms"], 4),
+                     "algorithmic_flop_per_launch": gemm["flop"]},
         "cpu_baseline": cpu,
         "gemv": gemv,
     }
