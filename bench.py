@@ -17,6 +17,12 @@ Also reported on the same JSON line:
     the 8 TB/s HBM peak.  The rotation is captured once in a HIP graph and
     replayed, so the figure is the kernels' own rate, not Python's launch
     rate;
+  * "flux_step": one FLUX.1-dev-shaped denoising-step forward at 1024^2
+    (19 double + 38 single blocks, hidden 3072,
+    4096 image + 512 text tokens, every linear Q4_K except the bf16 img_in),
+    built by mold_amd.flux on these quantized linears, in ms per step, with
+    its own host-CPU baseline (stems, one double block, one single block and
+    the final layer on the CPU, extrapolated x19 / x38 and labelled so);
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
     oracle/ and timed on a bounded row sample of the same workload on this
@@ -30,8 +36,9 @@ rocprofv3 counter summary profiles/gemm_q4k_linear1_traffic.md (FETCH_SIZE and
 WRITE_SIZE of `python3 bench.py --pmc-pass`, each scaled by what the counter
 reads for a plain copy of known size in the same run); null if absent.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv] [--no-flux]
        python bench.py --pmc-pass     (few launches of each kernel, for counters)
+       python bench.py --flux-only    (the FLUX step alone, for kernel traces)
 """
 from __future__ import annotations
 
@@ -158,6 +165,105 @@ def bench_gemv(dev, args):
     return out
 
 
+def bench_flux(dev, args):
+    """One FLUX.1-dev-shaped Q4_K step at 1024^2, eager, ms per step."""
+    import torch
+    from mold_amd import flux as F
+    cfg = F.FluxConfig.dev()
+    log("FLUX step: generating and quantizing the transformer's linears")
+    t0 = time.perf_counter()
+    params = F.FluxParams.random(cfg, dev, seed=4)
+    inp = F.make_inputs(cfg, 1024, 1024, 512, device="cuda", seed=4)
+    torch.cuda.synchronize()
+    log(f"  {len(params.lin)} quantized linears, {params.quantized_bytes() / 1e9:.2f} GB resident "
+        f"({time.perf_counter() - t0:.1f} s)")
+    step = F.FluxStep(params)
+    for _ in range(max(1, min(2, args.warmup))):
+        out = step.forward(**inp)
+    torch.cuda.synchronize()
+    n = max(3, min(10, args.steps // 4))
+    times = []
+    for _ in range(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = step.forward(**inp)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    assert torch.isfinite(out).all().item(), "non-finite FLUX step output"
+    lin, attn = F.step_flop(cfg, 4096, 512)
+    ms = sorted(times)[len(times) // 2]
+    log(f"  step {ms:.2f} ms (median of {n}), attention backend {F.ATTENTION_BACKEND['name']}")
+    res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
+           "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
+           "flop_linear": lin, "flop_attention": attn,
+           "weight_bytes": params.quantized_bytes(), "attention": F.ATTENTION_BACKEND["name"],
+           "config": "FLUX.1-dev shape, 1024x1024, batch 1, 4096 img + 512 txt tokens, Q4_K linears, "
+                     "f32 activations, bf16 GEMM inputs and attention"}
+    return res, params, inp
+
+
+class _CandleCpuLinear:
+    """A quantized linear on the host: candle's CPU QMatMul algorithm (oracle
+    restatement) on the same GGUF blocks, f32 in and out, bias added after."""
+
+    def __init__(self, lin, threads):
+        import torch
+        qt = lin.matmul.w
+        self.t, (self.n, self.k) = int(qt.dtype()), qt.shape
+        self.blocks = qt.data()
+        self.bias = lin.bias.cpu() if lin.bias is not None else None
+        self.threads = threads
+        self.torch = torch
+
+    def forward(self, x, act=0, out_dtype=None):
+        import numpy as np
+        from oracle import oracle as O
+        torch = self.torch
+        x2 = np.ascontiguousarray(x.float().reshape(-1, self.k).numpy())
+        y = torch.from_numpy(O.matmul_candle(self.t, x2, self.blocks, self.n, self.k, nthreads=self.threads))
+        if self.bias is not None:
+            y = y + self.bias
+        if act == 1:
+            y = torch.nn.functional.gelu(y, approximate="tanh")
+        return y.to(out_dtype or torch.float32)
+
+
+def cpu_flux_baseline(params, inp):
+    """Host-CPU FLUX step: stems, double block 0, single block 0 and the final
+    layer timed on the CPU, extrapolated to 19 + 38 blocks."""
+    import torch
+    from mold_amd import flux as F
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg = params.cfg
+    names = [nm for nm in params.lin if not nm.startswith(("double_blocks.", "single_blocks."))
+             or nm.startswith(("double_blocks.0.", "single_blocks.0."))]
+    lin = {nm: _CandleCpuLinear(params.lin[nm], threads) for nm in names}
+    dense = {nm: v.float().cpu() for nm, v in params.dense.items()
+             if not nm.startswith(("double_blocks.", "single_blocks.")) or ".0." in nm}
+    step = F.FluxStep(F.FluxParams(cfg, lin, dense), attn=F.attention_f32, gemm_dtype=torch.float32)
+    x = {k: v.cpu() for k, v in inp.items()}
+    t0 = time.perf_counter()
+    cos, sin = step.rope(x["img_ids"], x["txt_ids"])
+    img, txt, vec = step.stems(x["img"], x["txt"], x["t"], x["guidance"], x["y"])
+    t_stem = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    img, txt = step.double_block(0, img, txt, vec, cos, sin)
+    t_double = time.perf_counter() - t0
+    xs = torch.cat([txt, img], dim=0)
+    t0 = time.perf_counter()
+    xs = step.single_block(0, xs, vec, cos, sin)
+    t_single = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    step.final_layer(xs[txt.shape[0]:], vec)
+    t_final = time.perf_counter() - t0
+    total = t_stem + cfg.depth * t_double + cfg.depth_single_blocks * t_single + t_final
+    return {"value": round(total * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"extrapolated: stems {t_stem:.2f} s + 19 x double block {t_double:.2f} s + "
+                      f"38 x single block {t_single:.2f} s + final {t_final:.2f} s, each measured once "
+                      f"(quantized linears: candle CPU algorithm restated; glue and f32 attention: torch CPU)"}
+
+
 def read_traffic():
     """HBM bytes per GEMM launch from the committed counter summary, or None."""
     try:
@@ -227,6 +333,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
+    ap.add_argument("--no-flux", action="store_true")
+    ap.add_argument("--flux-only", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -241,10 +349,22 @@ def main():
     if args.pmc_pass:
         pmc_pass(dev, args)
         return
+    if args.flux_only:
+        flux, _, _ = bench_flux(dev, args)
+        print(json.dumps({"flux_step": flux}), flush=True)
+        return
     gemm, blocks, x = bench_gemm(dev, args)
     log(f"GEMM: {gemm['ms_per_step']:.3f} ms/step {gemm['tflops']:.1f} TFLOP/s; kernel {gemm['kernel_ms']:.3f} ms "
         f"{gemm['kernel_tflops']:.1f} TFLOP/s")
     gemv = None if args.no_gemv else bench_gemv(dev, args)
+    flux = None
+    if not args.no_flux:
+        flux, fparams, finp = bench_flux(dev, args)
+        if not args.no_cpu:
+            log("FLUX step CPU baseline (one block of each kind, extrapolated)")
+            flux["cpu_baseline"] = cpu_flux_baseline(fparams, finp)
+            log(f"  CPU: {flux['cpu_baseline']['value']:.0f} ms ({flux['cpu_baseline']['sample']})")
+        del fparams, finp
     cpu = None
     if not args.no_cpu:
         log("CPU baseline")
@@ -272,6 +392,7 @@ def main():
                      "algorithmic_flop_per_launch": gemm["flop"]},
         "cpu_baseline": cpu,
         "gemv": gemv,
+        "flux_step": flux,
     }
     print(json.dumps(line), flush=True)
 

@@ -1,0 +1,409 @@
+"""FLUX.1-dev-shaped transformer step whose linears are libmoldq quantized linears.
+
+This is the caller of the quantized-linear path that mold runs for quantized
+FLUX models: every `Linear` of the transformer is a GGUF weight driven by
+`QMatMul::forward` (here `mold_amd.Linear`), the glue (norms, modulation,
+RoPE, attention, residuals) is ordinary tensor work.  The block graph, its op
+order and constants follow mold's self-contained FLUX blocks,
+/root/reference/crates/mold-inference/src/flux/offload.rs:
+  timestep_embedding           :21-37   (t * 1000, 10000^(-i/half), [cos, sin])
+  attention / apply_rope       :39-73   (RoPE on pairs, softmax(q k^T / sqrt(d)) v)
+  LayerNorm without affine     :75-78   (eps 1e-6);  RmsNorm eps 1e-6 (:160-167)
+  Modulation1 / Modulation2    :105-156 (silu(vec) -> lin -> 3 / 6 chunks)
+  SelfAttention.qkv            :188-201 (reshape [L, 3, H, D], q/k RmsNorm)
+  Mlp                          :222-224 (lin1 -> gelu(tanh) -> lin2)
+  DoubleBlock.forward          :276-325 (txt tokens first in the joint sequence)
+  SingleBlock.forward          :374-392 (linear1 -> [qkv | mlp], linear2 on [attn | gelu(mlp)])
+  FinalLayer.forward           :413-422 (adaLN shift, scale; norm; linear)
+  forward (stems and order)    :523-574
+The position embedding is FLUX's EmbedNd (candle-transformers flux model,
+called at offload.rs:534-537): per axis i of the 3-D token ids, angles
+pos * theta^(-2j/d_i) for j < d_i/2, concatenated over axes, rotating each
+(even, odd) pair of q and k.
+
+Activations are f32, as in mold's quantized FLUX path
+(crates/mold-inference/src/flux/pipeline.rs:1524,1639-1647).  Two MI355X
+choices, both documented where they are made: a tensor whose only consumer is a
+quantized GEMM is produced directly in bf16 (the GEMM rounds its input to bf16
+with round-to-nearest-even either way, so results are identical and the f32 ->
+bf16 staging pass disappears), and attention runs in bf16 with f32 softmax
+accumulation (PyTorch's fused attention) rather than as three f32 ops.
+
+Weights are synthetic (no checkpoint exists here): every linear weight is
+N(0, 0.02^2) quantized on the GPU to the configured GGUF type, biases are f32
+N(0, 0.02^2), RmsNorm scales are bf16 N(1, 0.02^2), and `img_in` (K = 64 is not
+a multiple of a k-quant's 256-wide super-block) stays a dense bf16 weight.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Callable, Dict, Optional, Tuple
+
+from .quantized import ACT_GELU_TANH, ACT_NONE, GgmlDType, Linear, QTensor
+
+
+@dataclass(frozen=True)
+class FluxConfig:
+    """candle-transformers `flux::model::Config::dev()` shape."""
+    in_channels: int = 64
+    vec_in_dim: int = 768
+    context_in_dim: int = 4096
+    hidden_size: int = 3072
+    mlp_ratio: float = 4.0
+    num_heads: int = 24
+    depth: int = 19
+    depth_single_blocks: int = 38
+    axes_dim: Tuple[int, int, int] = (16, 56, 56)
+    theta: float = 10000.0
+    qkv_bias: bool = True
+    guidance_embed: bool = True
+
+    @property
+    def mlp_size(self) -> int:
+        return int(self.hidden_size * self.mlp_ratio)
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_heads
+
+    @staticmethod
+    def dev() -> "FluxConfig":
+        return FluxConfig()
+
+    @staticmethod
+    def tiny() -> "FluxConfig":
+        """Same graph at hidden 256 (2 heads of 128) with one block of each kind."""
+        return FluxConfig(vec_in_dim=256, context_in_dim=256, hidden_size=256, num_heads=2,
+                          depth=1, depth_single_blocks=1)
+
+
+def linear_shapes(cfg: FluxConfig) -> Dict[str, Tuple[int, int, bool]]:
+    """name -> (out_features, in_features, has_bias) for every quantized linear."""
+    h, mlp = cfg.hidden_size, cfg.mlp_size
+    s: Dict[str, Tuple[int, int, bool]] = {
+        "txt_in": (h, cfg.context_in_dim, True),
+        "time_in.in_layer": (h, 256, True), "time_in.out_layer": (h, h, True),
+        "vector_in.in_layer": (h, cfg.vec_in_dim, True), "vector_in.out_layer": (h, h, True),
+        "final_layer.adaLN_modulation.1": (2 * h, h, True),
+        "final_layer.linear": (cfg.in_channels, h, True),
+    }
+    if cfg.guidance_embed:
+        s["guidance_in.in_layer"] = (h, 256, True)
+        s["guidance_in.out_layer"] = (h, h, True)
+    for i in range(cfg.depth):
+        p = f"double_blocks.{i}."
+        for st in ("img", "txt"):
+            s[p + f"{st}_mod.lin"] = (6 * h, h, True)
+            s[p + f"{st}_attn.qkv"] = (3 * h, h, cfg.qkv_bias)
+            s[p + f"{st}_attn.proj"] = (h, h, True)
+            s[p + f"{st}_mlp.0"] = (mlp, h, True)
+            s[p + f"{st}_mlp.2"] = (h, mlp, True)
+    for i in range(cfg.depth_single_blocks):
+        p = f"single_blocks.{i}."
+        s[p + "modulation.lin"] = (3 * h, h, True)
+        s[p + "linear1"] = (3 * h + mlp, h, True)
+        s[p + "linear2"] = (h, h + mlp, True)
+    return s
+
+
+def dense_shapes(cfg: FluxConfig) -> Dict[str, Tuple[int, ...]]:
+    """Non-quantized parameters: img_in (bf16 weight, f32 bias) and RmsNorm scales."""
+    h, d = cfg.hidden_size, cfg.head_dim
+    s: Dict[str, Tuple[int, ...]] = {"img_in.weight": (h, cfg.in_channels), "img_in.bias": (h,)}
+    for i in range(cfg.depth):
+        for st in ("img", "txt"):
+            for nm in ("query_norm", "key_norm"):
+                s[f"double_blocks.{i}.{st}_attn.norm.{nm}.scale"] = (d,)
+    for i in range(cfg.depth_single_blocks):
+        for nm in ("query_norm", "key_norm"):
+            s[f"single_blocks.{i}.norm.{nm}.scale"] = (d,)
+    return s
+
+
+class FluxParams:
+    """The transformer's parameters: `lin[name]` objects with
+    `forward(x, act=ACT_NONE, out_dtype=None)` (bias applied inside), and
+    `dense[name]` tensors."""
+
+    def __init__(self, cfg: FluxConfig, lin: Dict[str, object], dense: Dict[str, object]):
+        self.cfg, self.lin, self.dense = cfg, lin, dense
+
+    @staticmethod
+    def random(cfg: FluxConfig, device, qtype: GgmlDType = GgmlDType.Q4_K, seed: int = 4) -> "FluxParams":
+        """Synthetic weights generated and quantized on `device` (a mold_amd.Device)."""
+        import torch
+        cuda = f"cuda:{device.ordinal}"
+        lin, dense = {}, {}
+        for idx, (name, (n, k, has_bias)) in enumerate(linear_shapes(cfg).items()):
+            g = torch.Generator(device=cuda).manual_seed(seed * 1_000_003 + 2 * idx)
+            w = torch.randn((n, k), device=cuda, generator=g) * 0.02
+            qt = QTensor.quantize(device, w, qtype)
+            del w
+            bias = None
+            if has_bias:
+                g = torch.Generator(device=cuda).manual_seed(seed * 1_000_003 + 2 * idx + 1)
+                bias = torch.randn((n,), device=cuda, generator=g) * 0.02
+            lin[name] = Linear(qt, bias)
+        for idx, (name, shape) in enumerate(dense_shapes(cfg).items()):
+            g = torch.Generator(device=cuda).manual_seed(seed * 7_000_003 + idx)
+            t = torch.randn(shape, device=cuda, generator=g) * 0.02
+            if name.endswith(".scale"):
+                t = (t + 1.0).to(torch.bfloat16)
+            elif name == "img_in.weight":
+                t = t.to(torch.bfloat16)
+            dense[name] = t
+        return FluxParams(cfg, lin, dense)
+
+    def quantized_bytes(self) -> int:
+        return sum(l.matmul.w.storage_size_in_bytes() for l in self.lin.values())
+
+
+# --------------------------------------------------------------------------- glue
+
+def timestep_embedding(t, dim: int):
+    """offload.rs:21-37.  t: [B] f32 -> [B, dim] f32."""
+    import torch
+    half = dim // 2
+    freqs = torch.exp(torch.arange(half, dtype=torch.float32, device=t.device) * (-math.log(10000.0) / half))
+    args = (t.float() * 1000.0)[:, None] * freqs[None, :]
+    return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+
+
+def rope_angles(ids, axes_dim, theta: float):
+    """EmbedNd angles: ids [L, n_axes] f32 -> [L, sum(axes_dim)/2] f32."""
+    import torch
+    parts = []
+    for i, d in enumerate(axes_dim):
+        inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float64, device=ids.device) / d))
+        parts.append(ids[:, i:i + 1].double() * inv[None, :])
+    return torch.cat(parts, dim=-1).float()
+
+
+def apply_rope(x, cos, sin):
+    """offload.rs:56-66: x [H, L, D]; pair (x[2j], x[2j+1]) rotated by angle j."""
+    x2 = x.reshape(*x.shape[:-1], -1, 2)
+    x0, x1 = x2[..., 0], x2[..., 1]
+    out = (cos * x0 - sin * x1, sin * x0 + cos * x1)
+    import torch
+    return torch.stack(out, dim=-1).reshape(x.shape)
+
+
+def rms_norm(x, scale):
+    import torch
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * scale.float()
+
+
+def layer_norm(x):
+    import torch
+    return torch.nn.functional.layer_norm(x, (x.shape[-1],), eps=1e-6)
+
+
+def gelu_tanh(x):
+    import torch
+    return torch.nn.functional.gelu(x, approximate="tanh")
+
+
+def silu(x):
+    import torch
+    return torch.nn.functional.silu(x)
+
+
+ATTENTION_BACKEND = {"name": None}
+
+
+def attention_bf16(q, k, v):
+    """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] f32 -> [L, H*D] bf16.
+
+    Runs PyTorch's fused flash / memory-efficient attention in bf16 (f32 softmax
+    accumulation inside).  Where neither fused kernel exists for the device, it
+    falls back to head-chunked bf16 products with f32 softmax; the right operand
+    of every batched product is made contiguous first (k^T explicitly), the form
+    that is safe for bf16 batched GEMMs on this platform.  The backend used is
+    recorded in ATTENTION_BACKEND."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    h, l, d = q.shape
+    qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    if ATTENTION_BACKEND["name"] in (None, "fused"):
+        try:
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
+            ATTENTION_BACKEND["name"] = "fused"
+            return o.transpose(0, 1).reshape(l, h * d)
+        except RuntimeError:
+            ATTENTION_BACKEND["name"] = "chunked"
+    out = torch.empty((l, h * d), dtype=torch.bfloat16, device=q.device)
+    scale = 1.0 / math.sqrt(d)
+    step = max(1, min(h, (1 << 31) // max(1, l * l * 4)))
+    for h0 in range(0, h, step):
+        h1 = min(h, h0 + step)
+        kt = kb[h0:h1].transpose(1, 2).contiguous()
+        s = torch.matmul(qb[h0:h1], kt).float() * scale
+        p = torch.softmax(s, dim=-1).to(torch.bfloat16)
+        o = torch.matmul(p, vb[h0:h1])
+        out.view(l, h, d)[:, h0:h1] = o.transpose(0, 1)
+    return out
+
+
+def attention_f32(q, k, v):
+    """Same in f32 (the host-CPU leg)."""
+    import torch
+    h, l, d = q.shape
+    o = torch.nn.functional.scaled_dot_product_attention(q[None], k[None], v[None])
+    return o[0].transpose(0, 1).reshape(l, h * d)
+
+
+class FluxStep:
+    """One denoising-step forward of the FLUX transformer (batch 1).
+
+    `attn` computes attention ([H, L, D] f32 x3 -> [L, H*D]); `gemm_dtype` is the
+    dtype in which tensors consumed only by a quantized linear are produced
+    (bf16 on the GPU, see the module docstring)."""
+
+    def __init__(self, params: FluxParams, attn: Callable = attention_bf16, gemm_dtype=None):
+        import torch
+        self.p, self.cfg = params, params.cfg
+        self.attn = attn
+        self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
+
+    # -- pieces, each following offload.rs
+    def _mod(self, name, vec, n):
+        y = self.p.lin[name].forward(silu(vec))
+        return y.chunk(n, dim=-1)
+
+    def _qkv(self, prefix, x, qn, kn):
+        cfg = self.cfg
+        L = x.shape[0]
+        qkv = self.p.lin[prefix + "qkv"].forward(x).reshape(L, 3, cfg.num_heads, cfg.head_dim)
+        q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[qn])
+        k = rms_norm(qkv[:, 1].transpose(0, 1), self.p.dense[kn])
+        v = qkv[:, 2].transpose(0, 1)
+        return q, k, v
+
+    def _modulate(self, x, shift, scale):
+        return (layer_norm(x) * (1.0 + scale) + shift).to(self.gemm_dtype)
+
+    def double_block(self, i, img, txt, vec, cos, sin):
+        p = f"double_blocks.{i}."
+        i_s1, i_c1, i_g1, i_s2, i_c2, i_g2 = self._mod(p + "img_mod.lin", vec, 6)
+        t_s1, t_c1, t_g1, t_s2, t_c2, t_g2 = self._mod(p + "txt_mod.lin", vec, 6)
+        iq, ik, iv = self._qkv(p + "img_attn.", self._modulate(img, i_s1, i_c1),
+                               p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")
+        tq, tk, tv = self._qkv(p + "txt_attn.", self._modulate(txt, t_s1, t_c1),
+                               p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale")
+        import torch
+        q = apply_rope(torch.cat([tq, iq], dim=1), cos, sin)
+        k = apply_rope(torch.cat([tk, ik], dim=1), cos, sin)
+        v = torch.cat([tv, iv], dim=1)
+        a = self.attn(q, k, v)
+        lt = txt.shape[0]
+        t_att, i_att = a[:lt], a[lt:]
+        img = img + i_g1 * self.p.lin[p + "img_attn.proj"].forward(i_att, out_dtype=torch.float32)
+        h = self.p.lin[p + "img_mlp.0"].forward(self._modulate(img, i_s2, i_c2), act=ACT_GELU_TANH,
+                                               out_dtype=self.gemm_dtype)
+        img = img + i_g2 * self.p.lin[p + "img_mlp.2"].forward(h, out_dtype=torch.float32)
+        txt = txt + t_g1 * self.p.lin[p + "txt_attn.proj"].forward(t_att, out_dtype=torch.float32)
+        h = self.p.lin[p + "txt_mlp.0"].forward(self._modulate(txt, t_s2, t_c2), act=ACT_GELU_TANH,
+                                               out_dtype=self.gemm_dtype)
+        txt = txt + t_g2 * self.p.lin[p + "txt_mlp.2"].forward(h, out_dtype=torch.float32)
+        return img, txt
+
+    def single_block(self, i, x, vec, cos, sin):
+        import torch
+        cfg = self.cfg
+        p = f"single_blocks.{i}."
+        shift, scale, gate = self._mod(p + "modulation.lin", vec, 3)
+        y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
+        L, h = x.shape[0], cfg.hidden_size
+        qkv = y[:, :3 * h].reshape(L, 3, cfg.num_heads, cfg.head_dim)
+        q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[p + "norm.query_norm.scale"])
+        k = rms_norm(qkv[:, 1].transpose(0, 1), self.p.dense[p + "norm.key_norm.scale"])
+        v = qkv[:, 2].transpose(0, 1)
+        a = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
+        cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
+        cat[:, :h] = a
+        cat[:, h:] = gelu_tanh(y[:, 3 * h:])
+        return x + gate * self.p.lin[p + "linear2"].forward(cat, out_dtype=torch.float32)
+
+    def stems(self, img, txt, t, guidance, y):
+        import torch
+        P = self.p
+        txt_h = P.lin["txt_in"].forward(txt.to(self.gemm_dtype), out_dtype=torch.float32)
+        img_h = torch.nn.functional.linear(img, P.dense["img_in.weight"].float(), P.dense["img_in.bias"])
+
+        def mlp_embed(prefix, x):
+            return P.lin[prefix + ".out_layer"].forward(silu(P.lin[prefix + ".in_layer"].forward(x)))
+        vec = mlp_embed("time_in", timestep_embedding(t, 256))
+        if self.cfg.guidance_embed:
+            vec = vec + mlp_embed("guidance_in", timestep_embedding(guidance, 256))
+        vec = vec + mlp_embed("vector_in", y)
+        return img_h, txt_h, vec
+
+    def final_layer(self, x, vec):
+        shift, scale = self.p.lin["final_layer.adaLN_modulation.1"].forward(silu(vec)).chunk(2, dim=-1)
+        import torch
+        return self.p.lin["final_layer.linear"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
+
+    def rope(self, img_ids, txt_ids):
+        import torch
+        ang = rope_angles(torch.cat([txt_ids, img_ids], dim=0), self.cfg.axes_dim, self.cfg.theta)
+        return torch.cos(ang), torch.sin(ang)
+
+    def forward(self, img, img_ids, txt, txt_ids, t, y, guidance=None, blocks: Optional[Tuple[int, int]] = None):
+        """img [L_img, in_channels], txt [L_txt, context_in_dim], y [1, vec_in_dim],
+        t and guidance [1]; ids [L, 3] f32.  Returns [L_img, in_channels] f32.
+        `blocks` = (double, single) limits the number of blocks run (host leg)."""
+        import torch
+        nd = self.cfg.depth if blocks is None else blocks[0]
+        ns = self.cfg.depth_single_blocks if blocks is None else blocks[1]
+        cos, sin = self.rope(img_ids, txt_ids)
+        img_h, txt_h, vec = self.stems(img, txt, t, guidance, y)
+        for i in range(nd):
+            img_h, txt_h = self.double_block(i, img_h, txt_h, vec, cos, sin)
+        x = torch.cat([txt_h, img_h], dim=0)
+        for i in range(ns):
+            x = self.single_block(i, x, vec, cos, sin)
+        return self.final_layer(x[txt_h.shape[0]:], vec)
+
+
+def make_inputs(cfg: FluxConfig, height: int = 1024, width: int = 1024, txt_len: int = 512,
+                device="cuda", seed: int = 4):
+    """Packed latents [(h/16)*(w/16), 64], ids, T5 states [txt_len, 4096], pooled
+    CLIP [1, 768], timestep 0.5, guidance 3.5, all N(0, 1) from `seed`."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(seed)
+    gh, gw = height // 16, width // 16
+    img = torch.randn((gh * gw, cfg.in_channels), device=device, generator=g)
+    txt = torch.randn((txt_len, cfg.context_in_dim), device=device, generator=g)
+    y = torch.randn((1, cfg.vec_in_dim), device=device, generator=g)
+    rows = torch.arange(gh, device=device, dtype=torch.float32)[:, None].expand(gh, gw)
+    cols = torch.arange(gw, device=device, dtype=torch.float32)[None, :].expand(gh, gw)
+    img_ids = torch.stack([torch.zeros_like(rows), rows, cols], dim=-1).reshape(-1, 3)
+    txt_ids = torch.zeros((txt_len, 3), device=device)
+    t = torch.full((1,), 0.5, device=device)
+    guidance = torch.full((1,), 3.5, device=device)
+    return dict(img=img, img_ids=img_ids, txt=txt, txt_ids=txt_ids, t=t, y=y, guidance=guidance)
+
+
+def step_flop(cfg: FluxConfig, l_img: int, l_txt: int) -> Tuple[float, float]:
+    """(linear FLOP with M > 1, attention FLOP) of one forward."""
+    L = l_img + l_txt
+    lin = 0.0
+    for name, (n, k, _) in linear_shapes(cfg).items():
+        if name.startswith("double_blocks"):
+            m = l_img if ".img_" in name else l_txt
+            m = 1 if name.endswith("_mod.lin") else m
+        elif name.startswith("single_blocks"):
+            m = 1 if name.endswith("modulation.lin") else L
+        elif name == "txt_in":
+            m = l_txt
+        elif name == "final_layer.linear":
+            m = l_img
+        else:
+            m = 1
+        if m > 1:
+            lin += 2.0 * m * n * k
+    blocks = cfg.depth + cfg.depth_single_blocks
+    attn = blocks * 2 * (2.0 * cfg.num_heads * L * L * cfg.head_dim)
+    return lin, attn
