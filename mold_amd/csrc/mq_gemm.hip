@@ -178,7 +178,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
 // Fast path (k % 256 == 0): 256 x 256 block tile, 8 waves (two per SIMD, so
 // one wave's dequant VALU work co-issues with the other's MFMAs), K step 64.
 //   * A (bf16 activations): 3-slot LDS ring filled by direct global->LDS
-//     loads (global_load_lds_dwordx4) two K steps ahead;
+//     loads (global_load_lds_dwordx4, inline asm) two K steps ahead;
 //   * B (weights): wave w decodes rows 32w..32w+31 of the block's 256 weight
 //     rows for the NEXT K step (per-type decoders, mq_bfrag.h) and writes the
 //     bf16 tile to a 2-slot LDS ring, so every weight is decoded once per
@@ -201,6 +201,20 @@ __device__ __forceinline__ void step_barrier(bool more) {
     asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One 1 KiB direct global->LDS load: lane i's 16 bytes from g land at LDS byte
+// address lds + 16 i.  Issued as inline asm so that the compiler does not see
+// an LDS write it cannot tell apart from the slot being read (it would wait
+// for every outstanding load before each LDS access, which turns the two-step
+// A prefetch into none); the kernel orders these loads with its own
+// s_waitcnt at the step barrier.  The compiler's waits for its own loads then
+// count fewer outstanding loads than there are, so they can only wait longer
+// than needed, never shorter.  M0 carries the LDS address (no other code in
+// these kernels uses M0); s_nop: one wait state between writing M0 and the
+// LDS-DMA instruction that reads it.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
 __device__ __forceinline__ int lds_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
@@ -256,18 +270,16 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     row = row < m ? row : m - 1;
     aoff[i] = row * lda + (((lane & 7) ^ ((r >> 1) & 7)) * 8);
   }
-  auto dma_a = [&](int64_t ks) {
-    uint4 *dst = &lds_a[ks % kAStages][(32 * wave) * 8];
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto dma_a = [&](uint4 *slot, int64_t ks) {
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void_t *)(slot + (32 * wave_u) * 8);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(static_cast<const void *>(a + aoff[i] + ks * kBK),
-                                       (lds_void_t *)(dst + 64 * i), 16, 0, 0);
+    for (int i = 0; i < 4; ++i) dma16(a + aoff[i] + ks * kBK, dst + 1024 * i);
   };
 
   typename TT::Raw raw;
   typename TT::Sc sc;
-  auto decode_to = [&]<int G>(int buf) {
-    uint4 *dst = lds_b[buf];
+  auto decode_to = [&]<int G>(uint4 *__restrict__ dst) {
     static_for<4>([&]<int S>() {
       const bf16x8 f = TT::template frag<G, S>(raw, sc);
       uint4 q;
@@ -279,14 +291,14 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   // prologue: unit 0's weight bytes, A(0), A(1); decode step 0
   TT::load_prep(raw, w, dt, drow, 0, h);
   static_for<kSteps>([&]<int G>() { TT::template reload<G>(raw, w, dt, drow, 0, h); });
-  dma_a(0);
-  if (ksteps > 1) dma_a(1);
+  dma_a(lds_a[0], 0);
+  if (ksteps > 1) dma_a(lds_a[1], 1);
   if (ksteps > 1)
     asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
   else
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   TT::prep(raw, sc, h);
-  decode_to.template operator()<0>(0);
+  decode_to.template operator()<0>(lds_b[0]);
   step_barrier(ksteps > 1);
 
   for (int64_t u = 0; u < units; ++u) {
@@ -295,21 +307,30 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
       const int64_t ks = u * kSteps + G;
       // the pieces decoded last iteration (step G of unit u) are free: fetch
       // unit u+1's; unit u's scales were unpacked last iteration too.
-      if (next_unit) {
-        TT::template reload<G>(raw, w, dt, drow, u + 1, h);
-        if constexpr (G == 0) TT::load_prep(raw, w, dt, drow, u + 1, h);
-      }
+      // Loads are issued unconditionally (the last unit re-reads itself, the
+      // last two steps re-fetch the final A step into a slot nobody reads), so
+      // the number of loads younger than any given one is the same on every
+      // path and the compiler's wait counts stay exact.
+      const int64_t un = next_unit ? u + 1 : u;
+      TT::template reload<G>(raw, w, dt, drow, un, h);
+      if constexpr (G == 0) TT::load_prep(raw, w, dt, drow, un, h);
       const bool more = ks + 2 < ksteps;
-      if (more) dma_a(ks + 2);
+      const int64_t ka = more ? ks + 2 : ksteps - 1;
+      // The step's four LDS slots (A being filled, A being read, B being
+      // decoded into, B being read) are distinct, which the restrict
+      // qualifiers tell the compiler.
+      auto body = [&](uint4 *__restrict__ a_dst, const uint4 *__restrict__ a_src, uint4 *__restrict__ b_dst,
+                      const uint4 *__restrict__ b_src) {
+      dma_a(a_dst, ka);
 
       // decode the next step's weights into the other B slot
       auto decode_next = [&]() {
         if constexpr (G + 1 < kSteps) {
-          decode_to.template operator()<G + 1>((int)((ks + 1) & 1));
+          decode_to.template operator()<G + 1>(b_dst);
         } else {
           if (next_unit) {
             TT::prep(raw, sc, h);
-            decode_to.template operator()<0>((int)((ks + 1) & 1));
+            decode_to.template operator()<0>(b_dst);
           }
         }
       };
@@ -317,8 +338,8 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
         // Every fragment row this lane reads has (row >> 1) & 7 == swz, so the
         // slot of slice S is fixed per lane and the 32-row tile offsets are
         // immediates: one address register per slice.
-        const char *abase = reinterpret_cast<const char *>(lds_a[ks % kAStages]) + (wm * 128 + l32) * 128;
-        const char *bbase = reinterpret_cast<const char *>(lds_b[ks & 1]) + (wn * 64 + l32) * 128;
+        const char *abase = reinterpret_cast<const char *>(a_src) + (wm * 128 + l32) * 128;
+        const char *bbase = reinterpret_cast<const char *>(b_src) + (wn * 64 + l32) * 128;
         bf16x8 fr[2][6];  // [slot][B nb=0,1 | A mb=0..3]
         auto read_frags = [&](bf16x8 *dst, int S) {
           const int off = (TT::chunk(S, h) ^ swz) * 16;
@@ -360,6 +381,8 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
         __builtin_amdgcn_sched_barrier(0);
         decode_next();
       }
+      };
+      body(lds_a[(ks + 2) % kAStages], lds_a[ks % kAStages], lds_b[(ks + 1) & 1], lds_b[ks & 1]);
       step_barrier(more);
     });
   }
