@@ -1,23 +1,26 @@
 // mq_gemm.hip — fused dequant -> bf16 MFMA GEMM for large-M quantized linears
 // (FLUX / Qwen-Image token projections): y[m, n] = act(x[m, :] . W[n, :] + b[n]).
 //
-// Tiling for gfx950 (256 CUs in 8 XCDs, 64-wide waves, 160 KiB LDS per CU):
-//   * workgroup = 4 waves, block tile 256 (m) x 256 (n), K step 64;
+// Both kernels tile for gfx950 (256 CUs in 8 XCDs, 64-wide waves, 160 KiB
+// LDS per CU) the same way:
+//   * workgroup = 4 waves (one per SIMD), block tile 256 (m) x 256 (n);
 //   * wave w owns weight tile nt*4 + w (64 output features) for all 256 rows,
 //     so every weight element is decoded exactly once per block tile and goes
 //     straight from registers into the MFMA B operand (no LDS round trip);
-//   * the bf16 activation tile 256 x 64 is staged through LDS (double
-//     buffered, XOR-swizzled 16-byte chunks, one barrier per K step) and read
-//     by all four waves;
+//   * the bf16 activation tile is staged through LDS (XOR-swizzled 16-byte
+//     chunks, one barrier per K step of 64) and read by all four waves;
 //   * v_mfma_f32_32x32x16_bf16: per wave 8 (m) x 2 (n) accumulator tiles,
 //     256 f32 accumulators per lane;
-//   * blockIdx -> tile mapping gives each XCD a contiguous run of tiles that
+//   * blockIdx -> tile mapping gives each XCD a contiguous range of tiles that
 //     share the same activation panel in its L2.
+// gemm_fast_kernel (k a multiple of 256) decodes with the per-type fragment
+// decoders of mq_bfrag.h and pipelines loads, decode and MFMAs; gemm_kernel
+// handles any k with the generic 8-element decoder.
 // Within a K step of 64, lane half h (lane / 32) supplies K elements
-// {16h..16h+15} u {32+16h..32+16h+15} (four runs of 8).  MFMA slice s takes
-// run c_s = (s/2)*4 + 2h + (s%2) of eight elements; the A operand reads the
-// same run from LDS, so the K order inside a step is a permutation shared by
-// both operands.
+// {16h..16h+15} u {32+16h..32+16h+15} (four runs of 8) in gemm_kernel, and
+// the per-type chunk order TT::chunk(s, h) in gemm_fast_kernel; the A operand
+// reads the same runs from LDS, so the K order inside a step is a permutation
+// shared by both operands.
 #include <utility>
 
 #include "mq_bfrag.h"
@@ -174,34 +177,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Fast path (k % 256 == 0): 256 x 256 block tile, 8 waves (two per SIMD, so
-// one wave's dequant VALU work co-issues with the other's MFMAs), K step 64.
-//   * A (bf16 activations): 3-slot LDS ring filled by direct global->LDS
-//     loads (global_load_lds_dwordx4, inline asm) two K steps ahead;
-//   * B (weights): wave w decodes rows 32w..32w+31 of the block's 256 weight
-//     rows for the NEXT K step (per-type decoders, mq_bfrag.h) and writes the
-//     bf16 tile to a 2-slot LDS ring, so every weight is decoded once per
-//     block tile; its packed bytes are reloaded into registers for the next
-//     unit one step after their last use;
-//   * MFMA: wave (wm = w&1, wn = w>>1) owns output rows 128wm.. and columns
-//     64wn..: 4 x 2 tiles of v_mfma_f32_32x32x16_bf16 per 16-K slice;
-//   * LDS rows are 128 B (64 bf16); 16-byte chunk c of row r sits in slot
-//     c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128 quarter (16
-//     consecutive rows) cover all 64 banks;
-//   * one barrier per step: s_waitcnt vmcnt(4) (the only younger memory ops
-//     are this step's four A loads) lgkmcnt(0), then s_barrier.
-constexpr int kAStages = 3;
 constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
-constexpr int kFastThreads = 512;
+constexpr int kFastThreads = 256;
 typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ void step_barrier(bool more) {
-  if (more)
-    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
 
 // One 1 KiB direct global->LDS load: lane i's 16 bytes from g land at LDS byte
 // address lds + 16 i.  Issued as inline asm so that the compiler does not see
@@ -217,7 +195,28 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
 
-__device__ __forceinline__ int lds_slot(int row, int chunk) { return row * 8 + (chunk ^ ((row >> 1) & 7)); }
+// ---------------------------------------------------------------------------
+// Fast path (k a multiple of the type's unit, 16-byte aligned activation
+// rows): one wave per SIMD, 256 x 256 block tile, 4 waves, K step 64.
+//   * wave w owns weight tile nt*4 + w (64 output features) for all 256 rows:
+//     lane (l32, h) decodes weight rows l32 and l32 + 32 of that tile straight
+//     into MFMA B operands (per-type decoders, mq_bfrag.h), so every weight
+//     is decoded once per block tile and B never touches LDS;
+//   * A (bf16 activations, 256 x 64 per step) goes global -> LDS by direct
+//     loads (dma16) into a 4-slot ring three steps ahead, one barrier per
+//     step; rows are 128 B with 16-byte chunk c of row r in slot
+//     c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128 quarter hit
+//     distinct banks;
+//   * with one wave per SIMD each wave has 512 registers: the 8 x 2 tiles of
+//     v_mfma_f32_32x32x16_bf16 accumulators (256 f32) sit in AGPRs, leaving
+//     room to read the next slice's A fragments and decode its B operands
+//     (the next step's first slice during the last slice) while the current
+//     slice's 16 MFMAs run;
+//   * XCD-aware tile order (workgroup i runs on XCD i % 8; each XCD gets a
+//     contiguous run of tiles, row-major over n, sharing the x panel in L2);
+//   * weight bytes for unit u+1 are fetched during unit u (one unit ahead);
+//     every load is unconditional (the last unit re-reads itself), so the
+//     compiler's wait counts are the same on every path.
 
 template <int TYPE, typename OUT>
 __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
@@ -225,8 +224,10 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act, int tiles_m, int tiles_n) {
   using TT = bfrag::T<TYPE>;
   constexpr int kSteps = TT::kUnitK / kBK;
-  __shared__ uint4 lds_a[kAStages][kBM * kBK / 8];
-  __shared__ uint4 lds_b[2][kBN * kBK / 8];
+  // VALU instructions placed after each pair of MFMAs (the decode work per
+  // MFMA differs by type; measured best per type)
+  constexpr int kVpm = TYPE == Q8_0 ? 3 : (TYPE == Q4_K || TYPE == Q5_K) ? 6 : 8;
+  __shared__ uint4 lds_a[4][kBM * kBK / 8];
 
   const int total = tiles_m * tiles_n;
   const int bid = blockIdx.x;
@@ -238,167 +239,143 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int phase = (wave >> 2) & 1;
-  const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane touches
+  const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
   const int64_t m0 = (int64_t)mt * kBM;
   const int64_t units = k / TT::kUnitK;
   const int64_t ksteps = units * kSteps;
+  const int64_t wt_raw = (int64_t)nt * (kBN / kRowTile) + wave;
+  const int64_t wt = wt_raw < ntiles_w ? wt_raw : ntiles_w - 1;  // keep reads in bounds
 
-  // decoder role: weight tile nt*4 + wave/2, row (wave&1)*32 + l32 of it
-  const int64_t dt_raw = (int64_t)nt * (kBN / kRowTile) + (wave >> 1);
-  const int64_t dt = dt_raw < ntiles_w ? dt_raw : ntiles_w - 1;  // keep reads in bounds
-  const int drow = (wave & 1) * 32 + l32;
-  const int brow = 32 * wave + l32;  // its row in the LDS B tile
-
-  f32x16 acc[4][2];
+  f32x16 acc[8][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // A DMA: load i (0..3) of wave w fills LDS rows 8(4w+i)..+7 (1 KiB); lane
-  // j fetches row 8(4w+i) + j/8, logical chunk (j&7) ^ ((row >> 1) & 7).
+  // A: 4-slot LDS ring filled by direct global->LDS loads three K steps
+  // ahead.  Load i (0..7) of wave w fills LDS rows 64w + 8i .. +7 (1 KiB);
+  // lane j fetches row 64w + 8i + j/8, logical chunk (j&7) ^ ((row>>1)&7).
   // Rows past m read row m-1 (finite, never stored).
-  int64_t aoff[4];
+  int aoff[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * (4 * wave + i) + (lane >> 3);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 64 * wave + 8 * i + (lane >> 3);
     int64_t row = m0 + r;
     row = row < m ? row : m - 1;
-    aoff[i] = row * lda + (((lane & 7) ^ ((r >> 1) & 7)) * 8);
+    aoff[i] = (int)(row * lda + (((lane & 7) ^ ((r >> 1) & 7)) * 8));
   }
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   auto dma_a = [&](uint4 *slot, int64_t ks) {
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void_t *)(slot + (32 * wave_u) * 8);
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void_t *)(slot + 64 * 8 * wave_u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(a + aoff[i] + ks * kBK, dst + 1024 * i);
+    for (int i = 0; i < 8; ++i) dma16(a + aoff[i] + ks * kBK, dst + 1024 * i);
   };
 
-  typename TT::Raw raw;
-  typename TT::Sc sc;
-  auto decode_to = [&]<int G>(uint4 *__restrict__ dst) {
-    static_for<4>([&]<int S>() {
-      const bf16x8 f = TT::template frag<G, S>(raw, sc);
-      uint4 q;
-      __builtin_memcpy(&q, &f, 16);
-      dst[brow * 8 + (TT::chunk(S, h) ^ swz)] = q;
-    });
+  typename TT::Raw raw[2];
+  typename TT::Sc sc[2];
+  // Barrier between K steps (global loads stay in flight across it, which
+  // __syncthreads would not allow).  At the end of step ks the A loads for step ks+1 (issued two steps
+  // earlier) must have landed; younger than them are at least the 16 loads
+  // for steps ks+2 and ks+3, so vmcnt(16) suffices and leaves the newest
+  // weight reloads in flight.
+  auto step_sync = [&]() { asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+  // A fragments of slice S from slot `slot`, and B operands of slice S of
+  // step G from the unpacked weight bytes.
+  bf16x8 af[2][8], bf[2][2];
+  auto read_a = [&](bf16x8 *dst, const uint4 *__restrict__ slot, int S) {
+    const char *abase = reinterpret_cast<const char *>(slot) + l32 * 128 + (TT::chunk(S, h) ^ swz) * 16;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) dst[mb] = *reinterpret_cast<const bf16x8 *>(abase + mb * 4096);
+  };
+  auto decode_b = [&]<int G, int S>(bf16x8 *dst) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dst[j] = TT::template frag<G, S>(raw[j], sc[j]);
   };
 
-  // prologue: unit 0's weight bytes, A(0), A(1); decode step 0
-  TT::load_prep(raw, w, dt, drow, 0, h);
-  static_for<kSteps>([&]<int G>() { TT::template reload<G>(raw, w, dt, drow, 0, h); });
+  // prologue: unit 0's weight bytes and scales, A(0) and A(1) into slots 0, 1;
+  // step 0's slice-0 operands
+#pragma unroll
+  for (int j = 0; j < 2; ++j) TT::load_prep(raw[j], w, wt, l32 + 32 * j, 0, h);
+  static_for<kSteps>([&]<int G>() {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, 0, h);
+  });
   dma_a(lds_a[0], 0);
-  if (ksteps > 1) dma_a(lds_a[1], 1);
-  if (ksteps > 1)
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  TT::prep(raw, sc, h);
-  decode_to.template operator()<0>(lds_b[0]);
-  step_barrier(ksteps > 1);
+  dma_a(lds_a[1], ksteps > 1 ? 1 : 0);
+  dma_a(lds_a[2], ksteps > 2 ? 2 : ksteps - 1);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) TT::prep(raw[j], sc[j], h);
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  read_a(af[0], lds_a[0], 0);
+  decode_b.template operator()<0, 0>(bf[0]);
 
   for (int64_t u = 0; u < units; ++u) {
-    const bool next_unit = u + 1 < units;
+    const int64_t un = u + 1 < units ? u + 1 : u;
     static_for<kSteps>([&]<int G>() {
       const int64_t ks = u * kSteps + G;
-      // the pieces decoded last iteration (step G of unit u) are free: fetch
-      // unit u+1's; unit u's scales were unpacked last iteration too.
-      // Loads are issued unconditionally (the last unit re-reads itself, the
-      // last two steps re-fetch the final A step into a slot nobody reads), so
-      // the number of loads younger than any given one is the same on every
-      // path and the compiler's wait counts stay exact.
-      const int64_t un = next_unit ? u + 1 : u;
-      TT::template reload<G>(raw, w, dt, drow, un, h);
-      if constexpr (G == 0) TT::load_prep(raw, w, dt, drow, un, h);
-      const bool more = ks + 2 < ksteps;
-      const int64_t ka = more ? ks + 2 : ksteps - 1;
-      // The step's four LDS slots (A being filled, A being read, B being
-      // decoded into, B being read) are distinct, which the restrict
-      // qualifiers tell the compiler.
-      auto body = [&](uint4 *__restrict__ a_dst, const uint4 *__restrict__ a_src, uint4 *__restrict__ b_dst,
-                      const uint4 *__restrict__ b_src) {
-      dma_a(a_dst, ka);
-
-      // decode the next step's weights into the other B slot
-      auto decode_next = [&]() {
-        if constexpr (G + 1 < kSteps) {
-          decode_to.template operator()<G + 1>(b_dst);
-        } else {
-          if (next_unit) {
-            TT::prep(raw, sc, h);
-            decode_to.template operator()<0>(b_dst);
-          }
-        }
-      };
-      auto mfma_step = [&]() {
-        // Every fragment row this lane reads has (row >> 1) & 7 == swz, so the
-        // slot of slice S is fixed per lane and the 32-row tile offsets are
-        // immediates: one address register per slice.
-        const char *abase = reinterpret_cast<const char *>(a_src) + (wm * 128 + l32) * 128;
-        const char *bbase = reinterpret_cast<const char *>(b_src) + (wn * 64 + l32) * 128;
-        bf16x8 fr[2][6];  // [slot][B nb=0,1 | A mb=0..3]
-        auto read_frags = [&](bf16x8 *dst, int S) {
-          const int off = (TT::chunk(S, h) ^ swz) * 16;
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) dst[nb] = *reinterpret_cast<const bf16x8 *>(bbase + off + nb * 4096);
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) dst[2 + mb] = *reinterpret_cast<const bf16x8 *>(abase + off + mb * 4096);
-        };
-        read_frags(fr[0], 0);
+      const int64_t kf = ks + 3 < ksteps ? ks + 3 : ksteps - 1;
+      auto body = [&](const uint4 *__restrict__ a_cur, const uint4 *__restrict__ a_next,
+                      uint4 *__restrict__ a_fill) {
+        dma_a(a_fill, kf);
         static_for<4>([&]<int S>() {
-          if constexpr (S < 3) read_frags(fr[(S + 1) & 1], S + 1);
+          // operands of the next slice (slice 0 of the next step after S = 3)
+          if constexpr (S < 3) {
+            read_a(af[(S + 1) & 1], a_cur, S + 1);
+            decode_b.template operator()<G, S + 1>(bf[(S + 1) & 1]);
+          } else {
+            // piece G is fully decoded: fetch unit u+1's (and its scale bytes
+            // after step 0); unit u+1's scales are unpacked before its first
+            // slice is decoded.
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb)
+            for (int j = 0; j < 2; ++j) {
+              TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, un, h);
+              if constexpr (G == 0) TT::load_prep(raw[j], w, wt, l32 + 32 * j, un, h);
+            }
+            read_a(af[0], a_next, 0);
+            if constexpr (G + 1 < kSteps) {
+              decode_b.template operator()<G + 1, 0>(bf[0]);
+            } else {
+#pragma unroll
+              for (int j = 0; j < 2; ++j) TT::prep(raw[j], sc[j], h);
+              decode_b.template operator()<0, 0>(bf[0]);
+            }
+          }
+#pragma unroll
+          for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
-              acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fr[S & 1][2 + mb], fr[S & 1][nb], acc[mb][nb], 0,
+              acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[S & 1][mb], bf[S & 1][nb], acc[mb][nb], 0,
                                                                     0, 0);
-          // interleave: the next slice's six fragment reads between this
-          // slice's eight MFMAs
-          if constexpr (S < 3) {
-            static_for<6>([&]<int I>() {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            });
+          static_for<8>([&]<int I>() {
             __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          } else {
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-          }
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kVpm, 0);
+          });
         });
       };
-      // The two waves sharing a SIMD (w and w+4) run the step's halves in
-      // opposite order, so one decodes (VALU) while the other runs MFMAs.
-      if (phase) {
-        decode_next();
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_step();
-      } else {
-        mfma_step();
-        __builtin_amdgcn_sched_barrier(0);
-        decode_next();
-      }
-      };
-      body(lds_a[(ks + 2) % kAStages], lds_a[ks % kAStages], lds_b[(ks + 1) & 1], lds_b[ks & 1]);
-      step_barrier(more);
+      body(lds_a[ks & 3], lds_a[(ks + 1) & 3], lds_a[(ks + 3) & 3]);
+      step_sync();
     });
   }
 
-  const int64_t wt_out = (int64_t)nt * (kBN / kRowTile) + wn;
-  if (wt_out >= ntiles_w) return;
-  const int64_t row0 = m0 + wm * 128 + 4 * h;
-  const int64_t col0 = wt_out * kRowTile + l32;
-  if (m0 + kBM <= m && wt_out * kRowTile + kRowTile <= n && act == MQ_ACT_NONE_) {
-    // full tile, no activation: unchecked stores
+  // no A load may still be in flight when the wave ends
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: lane holds column l32 of each 32x32 tile, rows
+  // 8*(e/4) + 4*h + (e%4).
+  if (wt_raw >= ntiles_w) return;
+  const int64_t row0 = m0 + 4 * h;
+  const int64_t col0 = wt_raw * kRowTile + l32;
+  if (m0 + kBM <= m && wt_raw * kRowTile + kRowTile <= n && act == MQ_ACT_NONE_) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const float bv = bias ? bias[col0 + nb * 32] : 0.f;
       OUT *yc = y + row0 * ldy + col0 + nb * 32;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
         for (int e = 0; e < 16; ++e)
           store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][nb][e] + bv);
@@ -411,7 +388,7 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     if (col >= n) continue;
     const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < 8; ++mb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
@@ -428,7 +405,9 @@ hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t n
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const int grid = tiles_m * tiles_n;
-  const bool fast = (k % 256) == 0 && lda % 8 == 0;
+  // fast path: whole 256-wide units, 16-byte aligned rows, and element
+  // offsets of x that fit the kernel's 32-bit row offsets
+  const bool fast = (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
   bool ok = dispatch_type(type, [&]<int T>() {
     if (fast) {
       if (y_type == F32)
