@@ -23,6 +23,11 @@ Also reported on the same JSON line:
     built by mold_amd.flux on these quantized linears, in ms per step, with
     its own host-CPU baseline (stems, one double block, one single block and
     the final layer on the CPU, extrapolated x19 / x38 and labelled so);
+  * "qwen_step": one Qwen-Image-shaped denoising-step forward at 1328^2
+    (60 dual-stream blocks, 6889 image + 256 text
+    tokens, q/k/v Q3_K, MLP Q2_K, out-projections and modulation Q4_K), built
+    by mold_amd.qwen_image, in ms per step, with a host-CPU baseline (stems,
+    block 0 and the output layer on the CPU, extrapolated x60);
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
     oracle/ and timed on a bounded row sample of the same workload on this
@@ -36,9 +41,10 @@ rocprofv3 counter summary profiles/gemm_q4k_linear1_traffic.md (FETCH_SIZE and
 WRITE_SIZE of `python3 bench.py --pmc-pass`, each scaled by what the counter
 reads for a plain copy of known size in the same run); null if absent.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv] [--no-flux]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv] [--no-flux] [--no-qwen]
        python bench.py --pmc-pass     (few launches of each kernel, for counters)
        python bench.py --flux-only    (the FLUX step alone, for kernel traces)
+       python bench.py --qwen-only    (the Qwen-Image step alone)
 """
 from __future__ import annotations
 
@@ -202,6 +208,80 @@ def bench_flux(dev, args):
     return res, params, inp
 
 
+def bench_qwen(dev, args):
+    """One Qwen-Image-shaped mixed low-bit step at 1328^2, eager, ms per step."""
+    import torch
+    from mold_amd import qwen_image as Q
+    from mold_amd.flux import ATTENTION_BACKEND
+    cfg = Q.QwenConfig.image()
+    log("Qwen-Image step: generating and quantizing the transformer's linears (Q3_K qkv, Q2_K MLP, Q4_K rest)")
+    t0 = time.perf_counter()
+    params = Q.QwenParams.random(cfg, dev, seed=5)
+    inp = Q.make_inputs(cfg, 1328, 1328, 256, device="cuda", seed=5)
+    torch.cuda.synchronize()
+    log(f"  {len(params.lin)} quantized linears, {params.quantized_bytes() / 1e9:.2f} GB resident "
+        f"({time.perf_counter() - t0:.1f} s)")
+    step = Q.QwenImageStep(params)
+    for _ in range(max(1, min(2, args.warmup))):
+        out = step.forward(**inp)
+    torch.cuda.synchronize()
+    n = max(3, min(10, args.steps // 4))
+    times = []
+    for _ in range(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = step.forward(**inp)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    assert torch.isfinite(out).all().item(), "non-finite Qwen step output"
+    l_img = inp["grid"][0] * inp["grid"][1]
+    lin, attn = Q.step_flop(cfg, l_img, 256)
+    ms = sorted(times)[len(times) // 2]
+    log(f"  step {ms:.2f} ms (median of {n}), attention backend {ATTENTION_BACKEND['name']}")
+    res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
+           "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
+           "flop_linear": lin, "flop_attention": attn,
+           "weight_bytes": params.quantized_bytes(), "attention": ATTENTION_BACKEND["name"],
+           "config": f"Qwen-Image shape, 1328x1328, batch 1, {l_img} img + 256 txt tokens, 60 blocks; "
+                     "q/k/v Q3_K (stacked per stream), MLP Q2_K, out-projections, modulation, stems Q4_K; "
+                     "f32 residuals, bf16 GEMM inputs and attention, text stream on a second HIP stream"}
+    return res, params, inp
+
+
+def cpu_qwen_baseline(params, inp):
+    """Host-CPU Qwen-Image step: stems, block 0 and the output layer timed on
+    the CPU, extrapolated to 60 blocks."""
+    import torch
+    from mold_amd import qwen_image as Q
+    from mold_amd.flux import attention_f32
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg = params.cfg
+    names = [nm for nm in params.lin if not nm.startswith("transformer_blocks.")
+             or nm.startswith("transformer_blocks.0.")]
+    lin = {nm: _CandleCpuLinear(params.lin[nm], threads) for nm in names}
+    dense = {nm: v.float().cpu() for nm, v in params.dense.items()
+             if not nm.startswith("transformer_blocks.") or nm.startswith("transformer_blocks.0.")}
+    step = Q.QwenImageStep(Q.QwenParams(cfg, lin, dense), attn=attention_f32, gemm_dtype=torch.float32,
+                           overlap=False)
+    x = {k: (v.cpu() if hasattr(v, "cpu") else v) for k, v in inp.items()}
+    t0 = time.perf_counter()
+    rope = Q.rope_tables(cfg, 1, x["grid"][0], x["grid"][1], x["txt"].shape[0], "cpu")
+    img, txt, temb = step.stems(x["img"], x["txt"], x["t"])
+    t_stem = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    img, txt = step.block(0, img, txt, Q.silu(temb), rope)
+    t_block = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    step.output_layer(img, temb)
+    t_out = time.perf_counter() - t0
+    total = t_stem + cfg.num_layers * t_block + t_out
+    return {"value": round(total * 1e3, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"extrapolated: stems {t_stem:.2f} s + 60 x block {t_block:.2f} s + output {t_out:.2f} s, "
+                      f"each measured once (quantized linears: candle CPU algorithm restated; glue and f32 "
+                      f"attention: torch CPU)"}
+
+
 class _CandleCpuLinear:
     """A quantized linear on the host: candle's CPU QMatMul algorithm (oracle
     restatement) on the same GGUF blocks, f32 in and out, bias added after."""
@@ -335,6 +415,8 @@ def main():
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-flux", action="store_true")
     ap.add_argument("--flux-only", action="store_true")
+    ap.add_argument("--no-qwen", action="store_true")
+    ap.add_argument("--qwen-only", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -353,6 +435,10 @@ def main():
         flux, _, _ = bench_flux(dev, args)
         print(json.dumps({"flux_step": flux}), flush=True)
         return
+    if args.qwen_only:
+        qwen, _, _ = bench_qwen(dev, args)
+        print(json.dumps({"qwen_step": qwen}), flush=True)
+        return
     gemm, blocks, x = bench_gemm(dev, args)
     log(f"GEMM: {gemm['ms_per_step']:.3f} ms/step {gemm['tflops']:.1f} TFLOP/s; kernel {gemm['kernel_ms']:.3f} ms "
         f"{gemm['kernel_tflops']:.1f} TFLOP/s")
@@ -365,6 +451,16 @@ def main():
             flux["cpu_baseline"] = cpu_flux_baseline(fparams, finp)
             log(f"  CPU: {flux['cpu_baseline']['value']:.0f} ms ({flux['cpu_baseline']['sample']})")
         del fparams, finp
+        torch.cuda.empty_cache()
+    qwen = None
+    if not args.no_qwen:
+        qwen, qparams, qinp = bench_qwen(dev, args)
+        if not args.no_cpu:
+            log("Qwen-Image step CPU baseline (one block, extrapolated)")
+            qwen["cpu_baseline"] = cpu_qwen_baseline(qparams, qinp)
+            log(f"  CPU: {qwen['cpu_baseline']['value']:.0f} ms ({qwen['cpu_baseline']['sample']})")
+        del qparams, qinp
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         log("CPU baseline")
@@ -393,6 +489,7 @@ def main():
         "cpu_baseline": cpu,
         "gemv": gemv,
         "flux_step": flux,
+        "qwen_step": qwen,
     }
     print(json.dumps(line), flush=True)
 

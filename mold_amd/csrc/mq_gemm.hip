@@ -28,6 +28,10 @@
 
 namespace mq {
 
+#ifdef MQ_GEMM_TYPE
+// Kernels of one weight type (this file is compiled once per type with
+// -DMQ_GEMM_TYPE=<type>, so the types build in parallel).
+
 constexpr int kBM = 256, kBN = 256, kBK = 64;
 constexpr int kGemmThreads = 256;
 
@@ -398,35 +402,50 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   }
 }
 
-hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,
-                       int64_t m, int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
-                       hipStream_t stream) {
-  if (m <= 0 || n <= 0) return hipSuccess;
+template <int T>
+hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
+                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
+                            hipStream_t stream) {
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const int grid = tiles_m * tiles_n;
   // fast path: whole 256-wide units, 16-byte aligned rows, and element
   // offsets of x that fit the kernel's 32-bit row offsets
   const bool fast = (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
-  bool ok = dispatch_type(type, [&]<int T>() {
-    if (fast) {
-      if (y_type == F32)
-        hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                           ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
-      else
-        hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                           ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
-      return;
-    }
+  if (fast) {
     if (y_type == F32)
-      hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k,
+      hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
                          ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
     else
-      hipLaunchKernelGGL((gemm_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k,
+      hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
                          ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
-  });
-  if (!ok) return hipErrorInvalidValue;
+  } else if (y_type == F32) {
+    hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
+                       a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
+                       a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
+  }
   return hipGetLastError();
 }
+
+template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64_t, int64_t, const __bf16 *,
+                                                   int64_t, int64_t, void *, int, int64_t, const float *, int,
+                                                   hipStream_t);
+
+#else  // the type dispatcher
+
+hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,
+                       int64_t m, int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
+                       hipStream_t stream) {
+  if (m <= 0 || n <= 0) return hipSuccess;
+  hipError_t err = hipErrorInvalidValue;
+  dispatch_type(type, [&]<int T>() {
+    err = launch_gemm_type<T>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, act, stream);
+  });
+  return err;
+}
+
+#endif  // MQ_GEMM_TYPE
 
 }  // namespace mq

@@ -38,6 +38,11 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const flo
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w,
                        const __bf16 *a, int64_t m, int64_t lda, void *y, int y_type, int64_t ldy,
                        const float *bias, int act, hipStream_t stream);
+// One weight type's launcher (instantiated in its own translation unit).
+template <int T>
+hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
+                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
+                            hipStream_t stream);
 
 // Epilogue activation (GELU with the tanh approximation, as candle's gelu()).
 __device__ __forceinline__ float apply_act(float v, int act) {

@@ -1,0 +1,389 @@
+"""Qwen-Image-shaped MMDiT step whose linears are libmoldq quantized linears.
+
+This is the second caller of the quantized-linear path: mold's quantized
+Qwen-Image transformer, /root/reference/crates/mold-inference/src/qwen_image/
+quantized_transformer.rs.  On CUDA mold runs each GGUF linear as a full
+dequantize to bf16 plus a dense matmul on every forward (`QwenLinear::Dequant`,
+:44-77); here every linear is `QMatMul::forward` on the resident GGUF blocks
+(the fused dequant GEMM), which is the replacement that file's Metal arm
+already uses (`QwenLinear::QMatMul`, :86-88).  Op order and constants follow:
+  TimestepProjEmbeddings.forward   :591-601 (10000^(-i/half), [cos, sin], lin1 -> silu -> lin2)
+  LayerNormNoParams                :126-158 (eps 1e-6, no affine)
+  DynamicRmsNorm                   :97-112  (x / sqrt(mean(x^2) + eps) * w)
+  QwenRopeEmbedder.forward         :339-435 (frame axis from 0, height/width axes centred
+                                             (-ceil(n/2) .. floor(n/2)-1), text from max(h/2, w/2))
+  JointAttention.forward           :695-781 (img: to_q/k/v, norm_q/k; txt: add_*_proj,
+                                             norm_added_q/k; RoPE; joint [txt, img]; to_out.0 and
+                                             to_add_out)
+  FeedForward                      :604-641 (net.0.proj -> gelu(tanh) -> net.2)
+  QwenImageTransformerBlock.forward:856-960 (silu(temb) -> img_mod.1 / txt_mod.1, 6 chunks
+                                             shift, scale, gate (msa), shift, scale, gate (mlp))
+  OutputLayer.forward              :977-989 (chunks scale, shift; norm; proj_out)
+  forward                          :1048-1139 (time embed, img_in, txt_norm -> txt_in, blocks)
+RoPE rotates interleaved pairs (x[2j], x[2j+1]) by angle j, candle's
+`z_image::transformer::apply_rotary_emb` (called at :742-745).
+
+Layout choices made here (the graph's values are unchanged by them):
+  * q, k and v of each stream are one weight: the rows of to_q, to_k, to_v
+    (or add_q_proj, add_k_proj, add_v_proj) stacked [3h, h].  GGUF rows are
+    independent, so the stacked blocks are the three tensors' blocks
+    concatenated, and y[:, :h], y[:, h:2h], y[:, 2h:] are the three outputs.
+    One GEMM with N = 9216 fills the chip where three with N = 3072 leave it
+    partly idle.
+  * The text stream's linears (M = 256 at 1328^2) run on a second HIP stream,
+    concurrently with the image stream's (M = 6889), joined by events before
+    the joint attention and at the end of each block.
+  * The residual streams stay f32; a tensor whose only consumer is a quantized
+    GEMM is produced in bf16 (the GEMM rounds its input to bf16 either way).
+  * The text attention mask is all ones for an unpadded prompt, which makes the
+    mask a no-op (:813-815 add 0 to every score), so none is applied.
+
+Weights are synthetic: every linear is N(0, 0.02^2) quantized on the GPU to the
+type `QwenConfig.qtypes` assigns (config 5: attention q/k/v Q3_K, MLP Q2_K,
+output projections and modulation Q4_K; stems and the output layer Q4_K),
+biases f32 N(0, 0.02^2), RmsNorm weights bf16 N(1, 0.02^2), `img_in` (K = 64,
+not a multiple of 256) a dense bf16 weight.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Callable, Dict, Optional, Tuple
+
+from .flux import apply_rope, attention_bf16, gelu_tanh, layer_norm, silu
+from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
+
+MAX_PERIOD = 10000.0
+
+
+@dataclass(frozen=True)
+class QwenConfig:
+    """Qwen-Image transformer shape (qwen_image/transformer.rs QwenImageConfig defaults)."""
+    in_channels: int = 64             # 16 latent channels x 2 x 2 patch
+    out_channels: int = 16
+    patch_size: int = 2
+    num_layers: int = 60
+    attention_head_dim: int = 128
+    num_attention_heads: int = 24
+    joint_attention_dim: int = 3584
+    mlp_hidden: int = 12288
+    axes_dims_rope: Tuple[int, int, int] = (16, 56, 56)
+    norm_eps: float = 1e-6
+    theta: float = 10000.0
+    # GGUF type per linear role (BASELINE config 5's mixed low-bit mapping)
+    qtypes: Tuple[Tuple[str, GgmlDType], ...] = field(default_factory=lambda: (
+        ("qkv", GgmlDType.Q3_K), ("mlp", GgmlDType.Q2_K), ("out", GgmlDType.Q4_K),
+        ("mod", GgmlDType.Q4_K), ("stem", GgmlDType.Q4_K)))
+
+    @property
+    def hidden_size(self) -> int:
+        return self.num_attention_heads * self.attention_head_dim
+
+    def qtype(self, role: str) -> GgmlDType:
+        return dict(self.qtypes)[role]
+
+    @staticmethod
+    def image() -> "QwenConfig":
+        return QwenConfig()
+
+    @staticmethod
+    def tiny() -> "QwenConfig":
+        """Same graph at hidden 256 (2 heads of 128), one block, small text dim."""
+        return QwenConfig(num_layers=1, num_attention_heads=2, joint_attention_dim=512, mlp_hidden=1024)
+
+
+def linear_shapes(cfg: QwenConfig) -> Dict[str, Tuple[int, int, str]]:
+    """name -> (out_features, in_features, role) for every quantized linear.
+    `attn.to_qkv` / `attn.add_qkv_proj` are the stacked q, k, v weights."""
+    h, mlp = cfg.hidden_size, cfg.mlp_hidden
+    s: Dict[str, Tuple[int, int, str]] = {
+        "time_text_embed.timestep_embedder.linear_1": (h, 256, "stem"),
+        "time_text_embed.timestep_embedder.linear_2": (h, h, "stem"),
+        "txt_in": (h, cfg.joint_attention_dim, "stem"),
+        "norm_out.linear": (2 * h, h, "stem"),
+        "proj_out": (cfg.patch_size ** 2 * cfg.out_channels, h, "stem"),
+    }
+    for i in range(cfg.num_layers):
+        p = f"transformer_blocks.{i}."
+        s[p + "img_mod.1"] = (6 * h, h, "mod")
+        s[p + "txt_mod.1"] = (6 * h, h, "mod")
+        s[p + "attn.to_qkv"] = (3 * h, h, "qkv")
+        s[p + "attn.add_qkv_proj"] = (3 * h, h, "qkv")
+        s[p + "attn.to_out.0"] = (h, h, "out")
+        s[p + "attn.to_add_out"] = (h, h, "out")
+        for st in ("img_mlp", "txt_mlp"):
+            s[p + f"{st}.net.0.proj"] = (mlp, h, "mlp")
+            s[p + f"{st}.net.2"] = (h, mlp, "mlp")
+    return s
+
+
+def dense_shapes(cfg: QwenConfig) -> Dict[str, Tuple[int, ...]]:
+    """Non-quantized parameters: img_in (bf16 weight, f32 bias) and RmsNorm weights."""
+    h, d = cfg.hidden_size, cfg.attention_head_dim
+    s: Dict[str, Tuple[int, ...]] = {"img_in.weight": (h, cfg.in_channels), "img_in.bias": (h,),
+                                     "txt_norm.weight": (cfg.joint_attention_dim,)}
+    for i in range(cfg.num_layers):
+        for nm in ("norm_q", "norm_k", "norm_added_q", "norm_added_k"):
+            s[f"transformer_blocks.{i}.attn.{nm}.weight"] = (d,)
+    return s
+
+
+class QwenParams:
+    """`lin[name]` objects with `forward(x, act=0, out_dtype=None)` (bias inside)
+    and `dense[name]` tensors."""
+
+    def __init__(self, cfg: QwenConfig, lin: Dict[str, object], dense: Dict[str, object]):
+        self.cfg, self.lin, self.dense = cfg, lin, dense
+
+    @staticmethod
+    def random(cfg: QwenConfig, device, seed: int = 5) -> "QwenParams":
+        """Synthetic weights generated and quantized on `device` (a mold_amd.Device)."""
+        import torch
+        cuda = f"cuda:{device.ordinal}"
+        lin, dense = {}, {}
+        for idx, (name, (n, k, role)) in enumerate(linear_shapes(cfg).items()):
+            g = torch.Generator(device=cuda).manual_seed(seed * 1_000_003 + 2 * idx)
+            w = torch.randn((n, k), device=cuda, generator=g) * 0.02
+            qt = QTensor.quantize(device, w, cfg.qtype(role))
+            del w
+            g = torch.Generator(device=cuda).manual_seed(seed * 1_000_003 + 2 * idx + 1)
+            lin[name] = Linear(qt, torch.randn((n,), device=cuda, generator=g) * 0.02)
+        for idx, (name, shape) in enumerate(dense_shapes(cfg).items()):
+            g = torch.Generator(device=cuda).manual_seed(seed * 7_000_003 + idx)
+            t = torch.randn(shape, device=cuda, generator=g) * 0.02
+            if name.endswith("norm_q.weight") or name.endswith("norm_k.weight") or "norm_added" in name \
+                    or name == "txt_norm.weight":
+                t = (t + 1.0).to(torch.bfloat16)
+            elif name == "img_in.weight":
+                t = t.to(torch.bfloat16)
+            dense[name] = t
+        return QwenParams(cfg, lin, dense)
+
+    def quantized_bytes(self) -> int:
+        return sum(l.matmul.w.storage_size_in_bytes() for l in self.lin.values())
+
+
+# --------------------------------------------------------------------------- glue
+
+def timestep_embedding(t, dim: int = 256):
+    """quantized_transformer.rs:591-599 (no 1000x scale: t is the scheduler timestep)."""
+    import torch
+    half = dim // 2
+    freqs = torch.exp(torch.arange(half, dtype=torch.float32, device=t.device) * (-math.log(MAX_PERIOD) / half))
+    args = t.float()[:, None] * freqs[None, :]
+    return torch.cat([torch.cos(args), torch.sin(args)], dim=-1)
+
+
+def rms_norm(x, w, eps: float = 1e-6):
+    import torch
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+
+
+def _axis_angles(pos, dim: int, theta: float):
+    """angles[p, j] = pos[p] * theta^(-2j/dim), j < dim/2."""
+    import torch
+    inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float64, device=pos.device) / dim))
+    return pos.double()[:, None] * inv[None, :]
+
+
+def rope_tables(cfg: QwenConfig, frames: int, height: int, width: int, txt_len: int, device):
+    """QwenRopeEmbedder.forward (:339-435): (img_cos, img_sin, txt_cos, txt_sin),
+    each [L, head_dim / 2] f32."""
+    import torch
+    fd, hd, wd = cfg.axes_dims_rope
+
+    def centred(n):
+        # negative half first: -(n - n//2) .. -1, then 0 .. n//2 - 1
+        return torch.cat([torch.arange(-(n - n // 2), 0, device=device),
+                          torch.arange(0, n // 2, device=device)]).double()
+
+    fa = _axis_angles(torch.arange(frames, device=device).double(), fd, cfg.theta)
+    ha = _axis_angles(centred(height), hd, cfg.theta)
+    wa = _axis_angles(centred(width), wd, cfg.theta)
+    img = torch.cat([fa[:, None, None, :].expand(frames, height, width, fd // 2),
+                     ha[None, :, None, :].expand(frames, height, width, hd // 2),
+                     wa[None, None, :, :].expand(frames, height, width, wd // 2)], dim=-1)
+    img = img.reshape(frames * height * width, -1)
+    start = max(height // 2, width // 2)
+    tp = torch.arange(start, start + txt_len, device=device).double()
+    txt = torch.cat([_axis_angles(tp, d, cfg.theta) for d in (fd, hd, wd)], dim=-1)
+    return (torch.cos(img).float(), torch.sin(img).float(), torch.cos(txt).float(), torch.sin(txt).float())
+
+
+def _aux_stream(device_index: int):
+    """One extra default-priority stream per device for the text-stream linears."""
+    import torch
+    s = _AUX.get(device_index)
+    if s is None:
+        s = torch.cuda.Stream(device=device_index)
+        _AUX[device_index] = s
+    return s
+
+
+_AUX: Dict[int, object] = {}
+
+
+class QwenImageStep:
+    """One denoising-step forward of the Qwen-Image transformer (batch 1).
+
+    `attn` computes attention ([H, L, D] f32 x3 -> [L, H*D]); `gemm_dtype` is the
+    dtype of tensors consumed only by a quantized linear; `overlap` runs the text
+    stream's work on a second HIP stream (GPU only)."""
+
+    def __init__(self, params: QwenParams, attn: Callable = attention_bf16, gemm_dtype=None,
+                 overlap: Optional[bool] = None):
+        import torch
+        self.p, self.cfg = params, params.cfg
+        self.attn = attn
+        self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
+        self.overlap = overlap
+
+    def _modulate(self, x, shift, scale):
+        return (layer_norm(x) * (1.0 + scale) + shift).to(self.gemm_dtype)
+
+    def _heads(self, y, qn, kn):
+        """[L, 3h] -> q, k (RmsNormed), v as [H, L, D] f32."""
+        cfg = self.cfg
+        L = y.shape[0]
+        y = y.reshape(L, 3, cfg.num_attention_heads, cfg.attention_head_dim)
+        q = rms_norm(y[:, 0].transpose(0, 1), self.p.dense[qn], cfg.norm_eps)
+        k = rms_norm(y[:, 1].transpose(0, 1), self.p.dense[kn], cfg.norm_eps)
+        return q, k, y[:, 2].transpose(0, 1).float()
+
+    def _txt_qkv(self, p, txt, mods, cos, sin):
+        t_s1, t_c1 = mods[0], mods[1]
+        import torch
+        y = self.p.lin[p + "attn.add_qkv_proj"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=torch.float32)
+        q, k, v = self._heads(y, p + "attn.norm_added_q.weight", p + "attn.norm_added_k.weight")
+        return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
+
+    def _txt_tail(self, p, txt, t_att, mods):
+        import torch
+        _, _, t_g1, t_s2, t_c2, t_g2 = mods
+        txt = txt + t_g1 * self.p.lin[p + "attn.to_add_out"].forward(t_att, out_dtype=torch.float32)
+        h = self.p.lin[p + "txt_mlp.net.0.proj"].forward(self._modulate(txt, t_s2, t_c2), act=ACT_GELU_TANH,
+                                                        out_dtype=self.gemm_dtype)
+        return txt + t_g2 * self.p.lin[p + "txt_mlp.net.2"].forward(h, out_dtype=torch.float32)
+
+    def block(self, i, img, txt, temb_silu, rope):
+        """QwenImageTransformerBlock.forward (:856-960)."""
+        import torch
+        p = f"transformer_blocks.{i}."
+        img_cos, img_sin, txt_cos, txt_sin = rope
+        i_mod_all = self.p.lin[p + "img_mod.1"].forward(temb_silu)
+        t_mod_all = self.p.lin[p + "txt_mod.1"].forward(temb_silu)
+        i_mod, t_mod = i_mod_all.chunk(6, dim=-1), t_mod_all.chunk(6, dim=-1)
+        aux = self._aux(img)
+        if aux is None:
+            tq, tk, tv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin)
+        else:
+            # text stream on `aux`: tensors made on one stream and read on the
+            # other are recorded on the reader, so the caching allocator does
+            # not hand their memory out again while the reader may still run.
+            main = torch.cuda.current_stream(img.device)
+            aux.wait_stream(main)
+            with torch.cuda.stream(aux):
+                tq, tk, tv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin)
+            for t in (txt, t_mod_all):
+                t.record_stream(aux)
+            for t in (tq, tk, tv):
+                t.record_stream(main)
+        y = self.p.lin[p + "attn.to_qkv"].forward(self._modulate(img, i_mod[0], i_mod[1]), out_dtype=torch.float32)
+        iq, ik, iv = self._heads(y, p + "attn.norm_q.weight", p + "attn.norm_k.weight")
+        iq, ik = apply_rope(iq, img_cos, img_sin), apply_rope(ik, img_cos, img_sin)
+        if aux is not None:
+            main.wait_stream(aux)
+        a = self.attn(torch.cat([tq, iq], dim=1), torch.cat([tk, ik], dim=1), torch.cat([tv, iv], dim=1))
+        lt = txt.shape[0]
+        t_att, i_att = a[:lt], a[lt:]
+        if aux is None:
+            txt = self._txt_tail(p, txt, t_att, t_mod)
+        else:
+            aux.wait_stream(main)
+            with torch.cuda.stream(aux):
+                txt_new = self._txt_tail(p, txt, t_att, t_mod)
+            for t in (txt, a, t_mod_all):
+                t.record_stream(aux)
+            txt = txt_new
+        _, _, i_g1, i_s2, i_c2, i_g2 = i_mod
+        img = img + i_g1 * self.p.lin[p + "attn.to_out.0"].forward(i_att, out_dtype=torch.float32)
+        h = self.p.lin[p + "img_mlp.net.0.proj"].forward(self._modulate(img, i_s2, i_c2), act=ACT_GELU_TANH,
+                                                        out_dtype=self.gemm_dtype)
+        img = img + i_g2 * self.p.lin[p + "img_mlp.net.2"].forward(h, out_dtype=torch.float32)
+        if aux is not None:
+            main.wait_stream(aux)
+            txt.record_stream(main)
+        return img, txt
+
+    def _aux(self, x):
+        """The text stream's HIP stream, or None to run everything in order.
+        Only with bf16 GEMM inputs: the linears then read their activations in
+        place and use none of the library context's shared staging scratch."""
+        import torch
+        use = self.overlap if self.overlap is not None else x.is_cuda
+        if not use or not x.is_cuda or self.gemm_dtype != torch.bfloat16:
+            return None
+        return _aux_stream(x.device.index if x.device.index is not None else torch.cuda.current_device())
+
+    def stems(self, img, txt, t):
+        import torch
+        P, cfg = self.p, self.cfg
+        e = timestep_embedding(t, 256)
+        temb = P.lin["time_text_embed.timestep_embedder.linear_2"].forward(
+            silu(P.lin["time_text_embed.timestep_embedder.linear_1"].forward(e)))
+        img_h = torch.nn.functional.linear(img, P.dense["img_in.weight"].float(), P.dense["img_in.bias"])
+        txt_n = rms_norm(txt, P.dense["txt_norm.weight"], cfg.norm_eps).to(self.gemm_dtype)
+        txt_h = P.lin["txt_in"].forward(txt_n, out_dtype=torch.float32)
+        return img_h, txt_h, temb
+
+    def output_layer(self, x, temb):
+        """OutputLayer.forward (:977-989): chunk 0 is scale, chunk 1 shift."""
+        import torch
+        scale, shift = self.p.lin["norm_out.linear"].forward(silu(temb)).chunk(2, dim=-1)
+        return self.p.lin["proj_out"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
+
+    def forward(self, img, txt, t, grid: Tuple[int, int], blocks: Optional[int] = None):
+        """img [H/2*W/2, 64] packed latents, txt [L_txt, joint_attention_dim], t [1];
+        grid = (H/2, W/2) in patches.  Returns [L_img, 64] f32.  `blocks` limits the
+        number of blocks run (host leg)."""
+        cfg = self.cfg
+        nb = cfg.num_layers if blocks is None else blocks
+        rope = rope_tables(cfg, 1, grid[0], grid[1], txt.shape[0], img.device)
+        img_h, txt_h, temb = self.stems(img, txt, t)
+        ts = silu(temb)
+        for i in range(nb):
+            img_h, txt_h = self.block(i, img_h, txt_h, ts, rope)
+        return self.output_layer(img_h, temb)
+
+
+def make_inputs(cfg: QwenConfig, height: int = 1328, width: int = 1328, txt_len: int = 256,
+                device="cuda", seed: int = 5):
+    """Packed latents [(h/16)*(w/16), 64] and text states [txt_len, 3584], N(0, 1);
+    timestep 500 (sigma 0.5 on the 0..1000 scale)."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(seed)
+    gh, gw = height // 16, width // 16
+    img = torch.randn((gh * gw, cfg.in_channels), device=device, generator=g)
+    txt = torch.randn((txt_len, cfg.joint_attention_dim), device=device, generator=g)
+    t = torch.full((1,), 500.0, device=device)
+    return dict(img=img, txt=txt, t=t, grid=(gh, gw))
+
+
+def step_flop(cfg: QwenConfig, l_img: int, l_txt: int) -> Tuple[float, float]:
+    """(linear FLOP with M > 1, attention FLOP) of one forward."""
+    L = l_img + l_txt
+    lin = 0.0
+    for name, (n, k, _) in linear_shapes(cfg).items():
+        if name.startswith("transformer_blocks"):
+            if name.endswith("_mod.1"):
+                continue
+            m = l_txt if (".add_" in name or "txt_mlp" in name or "to_add_out" in name) else l_img
+        elif name == "txt_in":
+            m = l_txt
+        elif name == "proj_out":
+            m = l_img
+        else:
+            continue
+        lin += 2.0 * m * n * k
+    attn = cfg.num_layers * 2 * (2.0 * cfg.num_attention_heads * L * L * cfg.attention_head_dim)
+    return lin, attn
