@@ -17,7 +17,6 @@
 
 namespace mq {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 template <int N, typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
@@ -110,7 +109,17 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K fast path (every skinny modulation linear of the FLUX / Qwen graphs).
+// Q4_K fast path (every skinny modulation linear of the FLUX / Qwen graphs):
+// candle's own QMatMul algorithm for k-quants.  x is quantized to Q8_K
+// (per 256 elements: iscale = -128 / (the element of largest magnitude, the
+// first one on ties), q = min(round_half_away(iscale * x), 127), d = 1 / iscale,
+// plus the sums of q over each 32-element sub-block), the weight nibbles
+// enter integer dot products exactly, and per super-block
+//   y += (d_w * d_x) * sum_s sc_s * sum_{i in s} q_w q_x
+//      - (dmin_w * d_x) * sum_s m_s * sum_{i in s} q_x,
+// the formula of candle's Q4_K x Q8_K vec_dot (k_quants.rs; restated in
+// oracle/ggml_oracle.c vd_q45_K).  The integer parts are exact, so the result
+// differs from candle's CPU path only in the order of the final f32 adds.
 //
 // Workgroup = R = 64/SL rows of one 64-row weight tile x all of K; wave w
 // takes super-blocks [w*SB, (w+1)*SB) (SB = 1 or 2 dividing K/256, at most
@@ -120,26 +129,23 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 // layout.  SL is picked so that the 64/R * tiles workgroups spread evenly
 // over the CUs; every output row's sum stays inside its workgroup (added in
 // fixed lane/wave order: deterministic, no cross-workgroup traffic).  All of
-// a wave's loads are issued first (x, scales, then chunks) so that staging x
-// waits only for x.
+// a wave's loads are issued first (x, scales, then chunks) so that the Q8_K
+// staging waits only for x.
 //
-// Arithmetic per 16-byte qs chunk (32 weights of one row: 16 low nibbles of
-// sub-block 2g, 16 high nibbles of sub-block 2g+1):
-//   * (w >> s) & 0x000F000F | 0x43004300 is a pair of bf16 values 128 + q
-//     (exact), one op per two weights;
-//   * v_dot2_f32_bf16 against x packed as bf16 pairs in the same nibble
-//     order gives S = sum (128 + q) x = 128 * X + sum q x, X = sum x over the
-//     16 weights;
-//   * y += d*sc * (S - 128 X) - dmin*m * X, i.e. two fmas per 16 weights.
-// x is rounded to bf16 (as in the GEMM's A operand); the weights enter exact.
-// Each wave stages its slice of x into LDS as bf16 pairs in nibble order
-// together with the 16-weight sums X.
+// Arithmetic per 16-byte qs chunk c of a super-block (32 weights of one row:
+// 16 low nibbles of sub-block 2g and 16 high nibbles of sub-block 2g+1,
+// g = c / 2, elements 64g + 16(c&1) + t and 64g + 32 + 16(c&1) + t):
+// word j's low nibbles (w & 0x0F0F0F0F) are elements 4j..4j+3 of the low run
+// in byte order, the high nibbles ((w >> 4) & 0x0F0F0F0F) those of the high
+// run, so each feeds one v_dot4_i32_i8 against four consecutive Q8_K bytes of
+// x: 3 + 2M VALU ops per 8 weights.
 constexpr int kQ4kMaxWaves = 16;
 constexpr size_t kQ4kMaxLds = 64 * 1024;
 
-// LDS bytes of the Q4_K GEMV: x pairs + sums for all K, and the reduction.
+// LDS bytes of the Q4_K GEMV: Q8_K x (256 quants, d, 8 sub-block sums per
+// super-block and row of x) for all K, and the reduction.
 static size_t q4k_lds_bytes(int64_t nb, int m) {
-  return (size_t)nb * 8 * m * (64 + 8) + (size_t)kQ4kMaxWaves * m * 64 * 4;
+  return (size_t)nb * m * (256 + 4 + 32) + (size_t)kQ4kMaxWaves * m * 64 * 4;
 }
 
 template <int M, int SB, int SL, typename OUT>
@@ -147,12 +153,13 @@ __global__ __launch_bounds__(kQ4kMaxWaves * 64) void gemv_q4k_kernel(
     WView w, int64_t n, int64_t nb, const float *__restrict__ x, int64_t ldx, OUT *__restrict__ y, int64_t ldy,
     const float *__restrict__ bias, int act) {
   constexpr int R = 64 / SL, CPL = 8 / SL;
-  extern __shared__ __align__(16) uint8_t smem[];
-  uint32_t(*xp)[M][16] = reinterpret_cast<uint32_t(*)[M][16]>(smem);                 // [chunk][m][16]
-  float2(*xsum)[M] = reinterpret_cast<float2(*)[M]>(smem + (size_t)nb * 8 * M * 64);  // [chunk][m]
-  float(*red)[M][64] = reinterpret_cast<float(*)[M][64]>(smem + (size_t)nb * 8 * M * 72);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint32_t(*xq)[M][64] = reinterpret_cast<uint32_t(*)[M][64]>(smem);                         // [sb][m][dword]
+  int32_t(*xb)[M][8] = reinterpret_cast<int32_t(*)[M][8]>(smem + (size_t)nb * M * 256);    // [sb][m][sub-block]
+  float(*xd)[M] = reinterpret_cast<float(*)[M]>(smem + (size_t)nb * M * 288);              // [sb][m]
+  float(*red)[M][64] = reinterpret_cast<float(*)[M][64]>(smem + (size_t)nb * M * 292);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int64_t tile = blockIdx.x / SL;
   const int rg = blockIdx.x - (int)(tile * SL);
   const int r = lane % R, sgrp = lane / R;
@@ -187,106 +194,128 @@ __global__ __launch_bounds__(kQ4kMaxWaves * 64) void gemv_q4k_kernel(
     for (int i = 0; i < CPL; ++i)
       q[sb][i] = bfrag::ld16(bfrag::chunk_at(w, 2, 8, tile, b0 + sb, sgrp * CPL + i, trow));
 
-  // 2. stage x: lane L packs weights 4L..4L+3 of each super-block: they are
-  //    bytes 4j..4j+3 (j = L & 3) of chunk c = 2(L >> 4) + ((L >> 2) & 1),
-  //    low nibbles if (L & 15) < 8, i.e. pair dwords 2j (x0, x2), 2j+1 (x1, x3).
-  {
-    const int c = 2 * (lane >> 4) + ((lane >> 2) & 1);
-    const int half = ((lane & 15) >> 3) * 8;
-    const int j = lane & 3;
+  // 2. Q8_K staging of this wave's super-blocks: lane L holds elements
+  //    4L..4L+3 (sub-block L / 8).
 #pragma unroll
-    for (int sb = 0; sb < SB; ++sb) {
-      const int64_t ch = (b0 + sb) * 8 + c;
+  for (int sb = 0; sb < SB; ++sb) {
+    const int64_t bg = b0 + sb;
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const __bf16 v0 = (__bf16)xv[sb][m][0], v1 = (__bf16)xv[sb][m][1];
-        const __bf16 v2 = (__bf16)xv[sb][m][2], v3 = (__bf16)xv[sb][m][3];
-        bf16x2_t p0 = {v0, v2}, p1 = {v1, v3};
-        uint2 pk;
-        __builtin_memcpy(&pk.x, &p0, 4);
-        __builtin_memcpy(&pk.y, &p1, 4);
-        *reinterpret_cast<uint2 *>(&xp[ch][m][half + 2 * j]) = pk;
-        float t = (float)v0 + (float)v1 + (float)v2 + (float)v3;
-        t += __shfl_xor(t, 1);
-        t += __shfl_xor(t, 2);
-        if (j == 0) {
-          if (half) xsum[ch][m].y = t;
-          else xsum[ch][m].x = t;
+    for (int m = 0; m < M; ++m) {
+      // largest magnitude over the wave, then the value of its first
+      // occurrence in element order (lowest lane, lowest slot in the lane)
+      const float a0 = __builtin_fabsf(xv[sb][m][0]), a1 = __builtin_fabsf(xv[sb][m][1]);
+      const float a2 = __builtin_fabsf(xv[sb][m][2]), a3 = __builtin_fabsf(xv[sb][m][3]);
+      float amax = __builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3));
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+      const float cand = a0 == amax ? xv[sb][m][0]
+                         : a1 == amax ? xv[sb][m][1]
+                         : a2 == amax ? xv[sb][m][2]
+                                      : xv[sb][m][3];
+      const uint64_t hit = __ballot(a0 == amax || a1 == amax || a2 == amax || a3 == amax);
+      const int first = hit ? __builtin_ctzll(hit) : 0;
+      const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), first));
+      uint32_t packed = 0;
+      int qsum = 0;
+      float dx = 0.f;
+      if (amax != 0.f) {
+        const float iscale = -128.f / vmax;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = (int)__builtin_fminf(__builtin_roundf(iscale * xv[sb][m][i]), 127.f);
+          qsum += v;
+          packed |= (uint32_t)(v & 0xFF) << (8 * i);
         }
+        dx = 1.f / iscale;
       }
+      xq[bg][m][lane] = packed;
+      qsum += __shfl_xor(qsum, 1);
+      qsum += __shfl_xor(qsum, 2);
+      qsum += __shfl_xor(qsum, 4);
+      if ((lane & 7) == 0) xb[bg][m][lane >> 3] = qsum;
+      if (lane == 0) xd[bg][m] = dx;
     }
   }
   __syncthreads();
 
-  // 3. dot products.  bf16 pair (128 + q, 128 + q').  Both constants live in
-  //    VGPRs: gfx9 VOP3 encodings take no literal and one scalar operand, so
-  //    only then does (v & mask) | bias become a single v_and_or_b32.
-  uint32_t kMask = 0x000F000Fu, kBias = 0x43004300u;
-  asm volatile("" : "+v"(kMask), "+v"(kBias));
-  float acc[M];
+  // 3. integer dot products, consumed in two halves of the chunk loads, each
+  //    behind its own wait, so the first half's arithmetic overlaps the
+  //    second half's loads.
+  int32_t S[SB][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.f;
-  // Chunks are consumed in two halves, each behind its own wait, so the
-  // first half's arithmetic overlaps the second half's loads (the compiler
-  // would otherwise wait for every chunk before the first dot product).
+  for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+    for (int m = 0; m < M; ++m) S[sb][m] = 0;
   constexpr int kLoads = SB * CPL, kFirst = kLoads / 2;  // chunks in the first half (may be 0)
   static_for<2>([&]<int HALF>() {
-    // chunk loads issued after the last chunk of this half
-    constexpr int after = HALF == 0 ? kLoads - kFirst : 0;
+    constexpr int after = HALF == 0 ? kLoads - kFirst : 0;  // chunk loads issued after this half
     constexpr int count = HALF == 0 ? kFirst : kLoads - kFirst;
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (0xF << 8) | (7 << 4));
     static_for<count>([&]<int LI>() {
       constexpr int li = (HALF == 0 ? 0 : kFirst) + LI;
       constexpr int sb = li / CPL, i = li % CPL;
-      const float d = h2f((uint16_t)(dm[sb] & 0xFFFF)), dmin = h2f((uint16_t)(dm[sb] >> 16));
       const int c = sgrp * CPL + i;  // compile-time when SL == 1
-      const int g = c >> 1;
+      const int g = c >> 1, hs = c & 1;
       // sub-blocks 2g (low nibbles) and 2g+1 (high): bytes (2g)&3, (2g+1)&3 of
-      // the packed 6-bit scale/min words for sub-blocks 0-3 (g < 2) or 4-7
+      // the packed 6-bit scale words for sub-blocks 0-3 (g < 2) or 4-7
       const uint32_t scw = g < 2 ? (s0[sb] & 0x3F3F3F3Fu) : ((s2[sb] & 0x0F0F0F0Fu) | ((s0[sb] >> 2) & 0x30303030u));
-      const uint32_t mw = g < 2 ? (s1[sb] & 0x3F3F3F3Fu) : (((s2[sb] >> 4) & 0x0F0F0F0Fu) | ((s1[sb] >> 2) & 0x30303030u));
       const int sh = 16 * (g & 1);
-      const float dlo = d * (float)((scw >> sh) & 0xFFu), dhi = d * (float)((scw >> (sh + 8)) & 0xFFu);
-      const float klo = __builtin_fmaf(128.f, dlo, dmin * (float)((mw >> sh) & 0xFFu));
-      const float khi = __builtin_fmaf(128.f, dhi, dmin * (float)((mw >> (sh + 8)) & 0xFFu));
+      const int sclo = (int)((scw >> sh) & 0xFFu), schi = (int)((scw >> (sh + 8)) & 0xFFu);
       const uint32_t wd[4] = {q[sb][i].x, q[sb][i].y, q[sb][i].z, q[sb][i].w};
-      uint32_t pl[8], ph[8];
+      uint32_t lo[4], hi[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        pl[2 * j] = (wd[j] & kMask) | kBias;
-        pl[2 * j + 1] = ((wd[j] >> 8) & kMask) | kBias;
-        ph[2 * j] = ((wd[j] >> 4) & kMask) | kBias;
-        ph[2 * j + 1] = ((wd[j] >> 12) & kMask) | kBias;
+        lo[j] = wd[j] & 0x0F0F0F0Fu;
+        hi[j] = (wd[j] >> 4) & 0x0F0F0F0Fu;
       }
-      const int64_t ch = (b0 + sb) * 8 + c;
+      const int64_t bg = b0 + sb;
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const uint4 *xr = reinterpret_cast<const uint4 *>(xp[ch][m]);
-        const uint4 xa = xr[0], xb = xr[1], xc = xr[2], xd = xr[3];
-        const uint32_t xl[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        const uint32_t xh[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
-        float sl = 0.f, sh2 = 0.f;
-#pragma unroll
-        for (int k2 = 0; k2 < 8; ++k2) {
-          bf16x2_t a, b;
-          __builtin_memcpy(&a, &pl[k2], 4);
-          __builtin_memcpy(&b, &xl[k2], 4);
-          sl = __builtin_amdgcn_fdot2_f32_bf16(a, b, sl, false);
-          __builtin_memcpy(&a, &ph[k2], 4);
-          __builtin_memcpy(&b, &xh[k2], 4);
-          sh2 = __builtin_amdgcn_fdot2_f32_bf16(a, b, sh2, false);
-        }
-        const float2 X = xsum[ch][m];
-        acc[m] = __builtin_fmaf(dlo, sl, acc[m]);
-        acc[m] = __builtin_fmaf(-klo, X.x, acc[m]);
-        acc[m] = __builtin_fmaf(dhi, sh2, acc[m]);
-        acc[m] = __builtin_fmaf(-khi, X.y, acc[m]);
+        const uint4 xa = *reinterpret_cast<const uint4 *>(&xq[bg][m][16 * g + 4 * hs]);
+        const uint4 xc = *reinterpret_cast<const uint4 *>(&xq[bg][m][16 * g + 8 + 4 * hs]);
+        int il = __builtin_amdgcn_sdot4((int)lo[0], (int)xa.x, 0, false);
+        il = __builtin_amdgcn_sdot4((int)lo[1], (int)xa.y, il, false);
+        il = __builtin_amdgcn_sdot4((int)lo[2], (int)xa.z, il, false);
+        il = __builtin_amdgcn_sdot4((int)lo[3], (int)xa.w, il, false);
+        int ih = __builtin_amdgcn_sdot4((int)hi[0], (int)xc.x, 0, false);
+        ih = __builtin_amdgcn_sdot4((int)hi[1], (int)xc.y, ih, false);
+        ih = __builtin_amdgcn_sdot4((int)hi[2], (int)xc.z, ih, false);
+        ih = __builtin_amdgcn_sdot4((int)hi[3], (int)xc.w, ih, false);
+        S[sb][m] += __mul24(sclo, il) + __mul24(schi, ih);  // |il|, |ih| < 2^15: 24-bit products are exact
       }
     });
   });
 
-  // 4. add the partial sums in lane-group, then wave order
+  // 4. per super-block f32 combine: (d_w d_x) S - (dmin_w d_x) sum_s m_s B_s,
+  //    the mins term once per row (lane group 0)
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) acc[m] = 0.f;
+#pragma unroll
+  for (int sb = 0; sb < SB; ++sb) {
+    const int64_t bg = b0 + sb;
+    const float d = h2f((uint16_t)(dm[sb] & 0xFFFF)), dmin = h2f((uint16_t)(dm[sb] >> 16));
+    const uint32_t mlo = s1[sb] & 0x3F3F3F3Fu;
+    const uint32_t mhi = ((s2[sb] >> 4) & 0x0F0F0F0Fu) | ((s1[sb] >> 2) & 0x30303030u);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const float dx = xd[bg][m];
+      int smin = 0;
+      if (sgrp == 0) {
+        const int4 ba = *reinterpret_cast<const int4 *>(&xb[bg][m][0]);
+        const int4 bb = *reinterpret_cast<const int4 *>(&xb[bg][m][4]);
+        smin = __mul24((int)(mlo & 0xFF), ba.x) + __mul24((int)((mlo >> 8) & 0xFF), ba.y) +
+               __mul24((int)((mlo >> 16) & 0xFF), ba.z) + __mul24((int)(mlo >> 24), ba.w) +
+               __mul24((int)(mhi & 0xFF), bb.x) + __mul24((int)((mhi >> 8) & 0xFF), bb.y) +
+               __mul24((int)((mhi >> 16) & 0xFF), bb.z) + __mul24((int)(mhi >> 24), bb.w);
+      }
+      acc[m] = __builtin_fmaf(d * dx, (float)S[sb][m], acc[m]);
+      acc[m] = __builtin_fmaf(-(dmin * dx), (float)smin, acc[m]);
+    }
+  }
+
+  // 5. add the partial sums in lane-group, then wave order
 #pragma unroll
   for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
   __syncthreads();
