@@ -122,6 +122,30 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
                int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
                const float *bias, int act, void *stream);
 
+/* --- Block glue between the quantized linears (fused row passes).  Both are
+ *     asynchronous on `stream` and allocate nothing. -------------------------- */
+
+/* out[r, :cols] = bf16(LayerNorm_eps(x[r, :cols]) * (1 + scale) + shift), the
+ * LayerNorm without affine weights; shift and scale are f32 [cols].  cols a
+ * multiple of 4, at most 8192; x 16-byte aligned, ldx and ldo multiples of 4.
+ * Replaces the modulate sequence of candle ops at
+ * crates/mold-inference/src/flux/offload.rs:283-286 (norm :75-78) and
+ * crates/mold-inference/src/qwen_image/quantized_transformer.rs:913-922. */
+int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, const float *shift,
+                      const float *scale, float eps, void *out, int64_t ldo, void *stream);
+
+/* For each of `rows` tokens and `heads` heads of the f32 projection output
+ * qkv[r, 0:3*heads*128] (row stride ld; q, k, v blocks of heads*128): RmsNorm
+ * of q and k (eps, bf16 weights [128]), RoPE rotating pair (2i, 2i+1) by the
+ * angle whose cos / sin are cos_table / sin_table[r, i] (f32 [rows, 64]), and
+ * q, k, v written as bf16 [heads, l_total, 128] at rows row_off .. row_off +
+ * rows - 1.  head_dim must be 128.  Replaces QkNorm + apply_rope + the head
+ * split at crates/mold-inference/src/flux/offload.rs:188-201, 56-66 and
+ * crates/mold-inference/src/qwen_image/quantized_transformer.rs:739-757. */
+int mq_qk_norm_rope(const float *qkv, int64_t ld, int64_t rows, int heads, int head_dim, const void *q_weight,
+                    const void *k_weight, float eps, const float *cos_table, const float *sin_table, void *q_out,
+                    void *k_out, void *v_out, int64_t row_off, int64_t l_total, void *stream);
+
 /* --- GGUF v2/v3 reader (candle gguf_file::Content::read, used at
  *     crates/mold-inference/src/flux/pipeline.rs:286-287). ------------------- */
 int mq_gguf_open(const char *path, mq_gguf **out);

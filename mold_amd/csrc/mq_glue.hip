@@ -1,0 +1,169 @@
+// mq_glue.hip — the two row-wise passes that sit between the quantized
+// linears of a DiT block, each fused into one HBM pass:
+//
+//   * mq_adaln_modulate: LayerNorm without affine (eps) of each row, times
+//     (1 + scale) plus shift, rounded once to bf16: the input of every
+//     attention / MLP linear (FLUX crates/mold-inference/src/flux/
+//     offload.rs:75-78 and :283-286, :374-377; Qwen-Image qwen_image/
+//     quantized_transformer.rs:913-922, :942-951).
+//   * mq_qk_norm_rope: per token and head, RmsNorm (eps, bf16 weight) of q and
+//     k, RoPE on interleaved pairs, and the head split of q, k and v into bf16
+//     [heads, L, 128] at a row offset of a joint sequence: what the qkv
+//     projection output goes through before attention (FLUX offload.rs:
+//     188-201 and :56-66; Qwen-Image quantized_transformer.rs:739-751).
+//
+// Both are HBM-bound (f32 in, bf16 out, a few flops per byte).
+#include "../../include/moldq.h"
+#include "mq_kernels.h"
+
+namespace mq {
+int set_error(int code, const char *msg);
+}
+
+using namespace mq;
+
+namespace {
+
+constexpr int kHead = 128;  // head dim: one wave holds a head as 64 (even, odd) pairs
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const __bf16 x = (__bf16)a, y = (__bf16)b;
+  uint16_t ux, uy;
+  __builtin_memcpy(&ux, &x, 2);
+  __builtin_memcpy(&uy, &y, 2);
+  return (uint32_t)ux | ((uint32_t)uy << 16);
+}
+
+// One wave per (token, head); lane i owns the pair (2i, 2i+1), which is also
+// RoPE's rotation pair i.  Four waves per workgroup.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const float *__restrict__ qkv, int64_t ld, int64_t rows, int heads, const __bf16 *__restrict__ qw,
+    const __bf16 *__restrict__ kw, float eps, const float *__restrict__ cosv, const float *__restrict__ sinv,
+    uint32_t *__restrict__ qo, uint32_t *__restrict__ ko, uint32_t *__restrict__ vo, int64_t row_off,
+    int64_t l_total) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= rows * heads) return;  // whole waves
+  const int64_t l = item / heads;
+  const int h = (int)(item - l * heads);
+  const float *src = qkv + l * ld + (int64_t)h * kHead + 2 * lane;
+  const float2 q = *reinterpret_cast<const float2 *>(src);
+  const float2 k = *reinterpret_cast<const float2 *>(src + (int64_t)heads * kHead);
+  const float2 v = *reinterpret_cast<const float2 *>(src + 2 * (int64_t)heads * kHead);
+  const float c = cosv[l * (kHead / 2) + lane], s = sinv[l * (kHead / 2) + lane];
+  const float rq = rsqrtf(wave_sum(q.x * q.x + q.y * q.y) / kHead + eps);
+  const float rk = rsqrtf(wave_sum(k.x * k.x + k.y * k.y) / kHead + eps);
+  const float q0 = q.x * rq * (float)qw[2 * lane], q1 = q.y * rq * (float)qw[2 * lane + 1];
+  const float k0 = k.x * rk * (float)kw[2 * lane], k1 = k.y * rk * (float)kw[2 * lane + 1];
+  const int64_t o = ((int64_t)h * l_total + row_off + l) * (kHead / 2) + lane;
+  qo[o] = pack_bf16x2(c * q0 - s * q1, s * q0 + c * q1);
+  ko[o] = pack_bf16x2(c * k0 - s * k1, s * k0 + c * k1);
+  vo[o] = pack_bf16x2(v.x, v.y);
+}
+
+// One workgroup of 256 threads per row; thread t owns float4 columns
+// t, t + 256, ... (at most kMaxVec of them).
+constexpr int kMaxVec = 8;  // cols <= 8192
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();  // red is reused between the two reductions
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void adaln_modulate_kernel(const float *__restrict__ x, int64_t ldx,
+                                                             int64_t cols, const float *__restrict__ shift,
+                                                             const float *__restrict__ scale, float eps,
+                                                             uint2 *__restrict__ out, int64_t ldo) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const int nv = (int)(cols / 4);
+  const float4 *xr = reinterpret_cast<const float4 *>(x + row * ldx);
+  float4 v[kMaxVec];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    v[j] = c < nv ? xr[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  }
+  const float mean = block_sum(s, red) / (float)cols;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    if (threadIdx.x + 256 * j < nv) {
+      const float a = v[j].x - mean, b = v[j].y - mean, c = v[j].z - mean, d = v[j].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float rstd = rsqrtf(block_sum(q, red) / (float)cols + eps);
+  uint2 *orow = out + row * (ldo / 4);
+#pragma unroll
+  for (int j = 0; j < kMaxVec; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nv) {
+      const float4 sc = reinterpret_cast<const float4 *>(scale)[c];
+      const float4 sh = reinterpret_cast<const float4 *>(shift)[c];
+      const float a = (v[j].x - mean) * rstd * (1.f + sc.x) + sh.x;
+      const float b = (v[j].y - mean) * rstd * (1.f + sc.y) + sh.y;
+      const float e = (v[j].z - mean) * rstd * (1.f + sc.z) + sh.z;
+      const float f = (v[j].w - mean) * rstd * (1.f + sc.w) + sh.w;
+      orow[c] = make_uint2(pack_bf16x2(a, b), pack_bf16x2(e, f));
+    }
+  }
+}
+
+int invalid(const char *msg) { return set_error(MQ_E_INVALID, msg); }
+
+bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int mq_qk_norm_rope(const float *qkv, int64_t ld, int64_t rows, int heads, int head_dim, const void *q_weight,
+                    const void *k_weight, float eps, const float *cos_table, const float *sin_table, void *q_out,
+                    void *k_out, void *v_out, int64_t row_off, int64_t l_total, void *stream) {
+  if (head_dim != kHead) return invalid("mq_qk_norm_rope: head_dim must be 128");
+  if (rows < 0 || heads <= 0 || row_off < 0 || row_off + rows > l_total)
+    return invalid("mq_qk_norm_rope: rows, heads or row range out of bounds");
+  if (ld < 3 * (int64_t)heads * kHead || ld % 2) return invalid("mq_qk_norm_rope: ld must be even and >= 3*heads*128");
+  if (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || !q_out || !k_out || !v_out)
+    return invalid("mq_qk_norm_rope: NULL pointer");
+  if (!aligned(qkv, 8) || !aligned(q_out, 4) || !aligned(k_out, 4) || !aligned(v_out, 4))
+    return invalid("mq_qk_norm_rope: misaligned buffer");
+  if (rows == 0) return MQ_OK;
+  const int64_t items = rows * heads;
+  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), qkv, ld, rows, heads, static_cast<const __bf16 *>(q_weight),
+                     static_cast<const __bf16 *>(k_weight), eps, cos_table, sin_table, static_cast<uint32_t *>(q_out),
+                     static_cast<uint32_t *>(k_out), static_cast<uint32_t *>(v_out), row_off, l_total);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
+}
+
+int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, const float *shift,
+                      const float *scale, float eps, void *out, int64_t ldo, void *stream) {
+  if (rows < 0 || cols <= 0 || cols % 4 || cols > 4 * 256 * kMaxVec)
+    return invalid("mq_adaln_modulate: cols must be a positive multiple of 4, at most 8192");
+  if (ldx < cols || ldo < cols || ldx % 4 || ldo % 4) return invalid("mq_adaln_modulate: bad row strides");
+  if (!x || !shift || !scale || !out) return invalid("mq_adaln_modulate: NULL pointer");
+  if (!aligned(x, 16) || !aligned(shift, 16) || !aligned(scale, 16) || !aligned(out, 8))
+    return invalid("mq_adaln_modulate: misaligned buffer");
+  if (rows == 0) return MQ_OK;
+  hipLaunchKernelGGL(adaln_modulate_kernel, dim3((unsigned)rows), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                     ldx, cols, shift, scale, eps, static_cast<uint2 *>(out), ldo);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
+}
+
+}  // extern "C"

@@ -22,12 +22,14 @@ pos * theta^(-2j/d_i) for j < d_i/2, concatenated over axes, rotating each
 (even, odd) pair of q and k.
 
 Activations are f32, as in mold's quantized FLUX path
-(crates/mold-inference/src/flux/pipeline.rs:1524,1639-1647).  Two MI355X
-choices, both documented where they are made: a tensor whose only consumer is a
-quantized GEMM is produced directly in bf16 (the GEMM rounds its input to bf16
-with round-to-nearest-even either way, so results are identical and the f32 ->
-bf16 staging pass disappears), and attention runs in bf16 with f32 softmax
-accumulation (PyTorch's fused attention) rather than as three f32 ops.
+(crates/mold-inference/src/flux/pipeline.rs:1524,1639-1647).  MI355X
+choices, each documented where it is made: on the GPU the modulate and the
+q/k norm + RoPE + head split run as libmoldq's fused row passes
+(mold_amd.fused), one HBM pass each instead of a dozen elementwise ops; a
+tensor whose only consumer is a quantized GEMM is produced directly in bf16
+(the GEMM rounds its input to bf16 with round-to-nearest-even either way, so
+the f32 -> bf16 staging pass disappears); and attention runs in bf16 with f32
+softmax accumulation (PyTorch's fused attention) rather than as three f32 ops.
 
 Weights are synthetic (no checkpoint exists here): every linear weight is
 N(0, 0.02^2) quantized on the GPU to the configured GGUF type, biases are f32
@@ -261,11 +263,21 @@ class FluxStep:
     dtype in which tensors consumed only by a quantized linear are produced
     (bf16 on the GPU, see the module docstring)."""
 
-    def __init__(self, params: FluxParams, attn: Callable = attention_bf16, gemm_dtype=None):
+    def __init__(self, params: FluxParams, attn: Callable = attention_bf16, gemm_dtype=None,
+                 fused: Optional[bool] = None):
         import torch
         self.p, self.cfg = params, params.cfg
         self.attn = attn
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
+        self.fused = fused
+
+    def _fused(self, x) -> bool:
+        """Use libmoldq's fused row passes (mold_amd.fused) for the modulate and the
+        q/k norm + RoPE + head split: by default on the GPU with bf16 GEMM inputs."""
+        import torch
+        if self.fused is not None:
+            return self.fused
+        return x.is_cuda and self.gemm_dtype == torch.bfloat16
 
     # -- pieces, each following offload.rs
     def _mod(self, name, vec, n):
@@ -282,20 +294,46 @@ class FluxStep:
         return q, k, v
 
     def _modulate(self, x, shift, scale):
+        if self._fused(x):
+            from .fused import adaln_modulate
+            return adaln_modulate(x, shift, scale)
         return (layer_norm(x) * (1.0 + scale) + shift).to(self.gemm_dtype)
+
+    def _heads_fused(self, segments, cos, sin):
+        """q, k, v bf16 [H, L, D] of the joint sequence from (qkv f32 [L_seg, >= 3h],
+        query-norm name, key-norm name) segments in sequence order."""
+        from .fused import new_heads, qk_norm_rope
+        total = sum(y.shape[0] for y, _, _ in segments)
+        q, k, v = new_heads(self.cfg.num_heads, total, segments[0][0].device)
+        off = 0
+        for y, qn, kn in segments:
+            n = y.shape[0]
+            qk_norm_rope(y, self.cfg.num_heads, self.p.dense[qn], self.p.dense[kn], cos[off:off + n],
+                         sin[off:off + n], q, k, v, off)
+            off += n
+        return q, k, v
 
     def double_block(self, i, img, txt, vec, cos, sin):
         p = f"double_blocks.{i}."
         i_s1, i_c1, i_g1, i_s2, i_c2, i_g2 = self._mod(p + "img_mod.lin", vec, 6)
         t_s1, t_c1, t_g1, t_s2, t_c2, t_g2 = self._mod(p + "txt_mod.lin", vec, 6)
-        iq, ik, iv = self._qkv(p + "img_attn.", self._modulate(img, i_s1, i_c1),
-                               p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")
-        tq, tk, tv = self._qkv(p + "txt_attn.", self._modulate(txt, t_s1, t_c1),
-                               p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale")
         import torch
-        q = apply_rope(torch.cat([tq, iq], dim=1), cos, sin)
-        k = apply_rope(torch.cat([tk, ik], dim=1), cos, sin)
-        v = torch.cat([tv, iv], dim=1)
+        if self._fused(img):
+            f32 = torch.float32
+            ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=f32)
+            iy = self.p.lin[p + "img_attn.qkv"].forward(self._modulate(img, i_s1, i_c1), out_dtype=f32)
+            q, k, v = self._heads_fused(
+                [(ty, p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale"),
+                 (iy, p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")], cos, sin)
+            del ty, iy
+        else:
+            iq, ik, iv = self._qkv(p + "img_attn.", self._modulate(img, i_s1, i_c1),
+                                   p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")
+            tq, tk, tv = self._qkv(p + "txt_attn.", self._modulate(txt, t_s1, t_c1),
+                                   p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale")
+            q = apply_rope(torch.cat([tq, iq], dim=1), cos, sin)
+            k = apply_rope(torch.cat([tk, ik], dim=1), cos, sin)
+            v = torch.cat([tv, iv], dim=1)
         a = self.attn(q, k, v)
         lt = txt.shape[0]
         t_att, i_att = a[:lt], a[lt:]
@@ -316,11 +354,14 @@ class FluxStep:
         shift, scale, gate = self._mod(p + "modulation.lin", vec, 3)
         y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
         L, h = x.shape[0], cfg.hidden_size
-        qkv = y[:, :3 * h].reshape(L, 3, cfg.num_heads, cfg.head_dim)
-        q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[p + "norm.query_norm.scale"])
-        k = rms_norm(qkv[:, 1].transpose(0, 1), self.p.dense[p + "norm.key_norm.scale"])
-        v = qkv[:, 2].transpose(0, 1)
-        a = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
+        if self._fused(x):
+            a = self.attn(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")], cos, sin))
+        else:
+            qkv = y[:, :3 * h].reshape(L, 3, cfg.num_heads, cfg.head_dim)
+            q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[p + "norm.query_norm.scale"])
+            k = rms_norm(qkv[:, 1].transpose(0, 1), self.p.dense[p + "norm.key_norm.scale"])
+            v = qkv[:, 2].transpose(0, 1)
+            a = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
         cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
         cat[:, :h] = a
         cat[:, h:] = gelu_tanh(y[:, 3 * h:])

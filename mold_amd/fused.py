@@ -1,0 +1,65 @@
+"""Fused block glue on the device: libmoldq's row passes between the quantized
+linears (mq_adaln_modulate, mq_qk_norm_rope in include/moldq.h).
+
+Both run on torch's current stream and allocate only their outputs.  They need
+the HIP library (no fallback); the host-CPU path of the block graphs keeps the
+equivalent torch ops.
+"""
+from __future__ import annotations
+
+from . import _lib
+from ._lib import check
+from .quantized import _stream_ptr
+
+HEAD_DIM = 128
+
+
+def adaln_modulate(x, shift, scale, eps: float = 1e-6, out=None):
+    """bf16(LayerNorm_eps(x) * (1 + scale) + shift) for x f32 [rows, cols] (row
+    stride x.stride(0)), shift and scale f32 with cols elements."""
+    import torch
+    if x.dtype != torch.float32 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("adaln_modulate: x must be a 2-D f32 tensor with unit column stride")
+    rows, cols = x.shape
+    shift = shift.reshape(-1)
+    scale = scale.reshape(-1)
+    for t in (shift, scale):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != cols:
+            raise ValueError("adaln_modulate: shift and scale must be contiguous f32 with cols elements")
+    if out is None:
+        out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
+    check(_lib.load().mq_adaln_modulate(x.data_ptr(), rows, cols, x.stride(0), shift.data_ptr(), scale.data_ptr(),
+                                        float(eps), out.data_ptr(), out.stride(0), _stream_ptr()))
+    return out
+
+
+def new_heads(heads: int, l_total: int, device):
+    """Empty bf16 q, k, v buffers [heads, l_total, 128] for qk_norm_rope."""
+    import torch
+    return tuple(torch.empty((heads, l_total, HEAD_DIM), dtype=torch.bfloat16, device=device) for _ in range(3))
+
+
+def qk_norm_rope(qkv, heads: int, q_weight, k_weight, cos, sin, q_out, k_out, v_out, row_off: int,
+                 eps: float = 1e-6):
+    """RmsNorm(q), RmsNorm(k), RoPE and the head split of one segment's projection
+    output qkv f32 [rows, >= 3*heads*128] (q | k | v column blocks) into bf16
+    [heads, l_total, 128] at rows row_off ..; cos / sin f32 [rows, 64] for the
+    segment's tokens; q_weight / k_weight bf16 [128]."""
+    import torch
+    if qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qk_norm_rope: qkv must be a 2-D f32 tensor with unit column stride")
+    rows = qkv.shape[0]
+    for t in (cos, sin):
+        if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (rows, HEAD_DIM // 2):
+            raise ValueError("qk_norm_rope: cos / sin must be contiguous f32 [rows, 64]")
+    for t in (q_weight, k_weight):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.numel() != HEAD_DIM:
+            raise ValueError("qk_norm_rope: norm weights must be contiguous bf16 [128]")
+    l_total = q_out.shape[1]
+    for t in (q_out, k_out, v_out):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != (heads, l_total, HEAD_DIM):
+            raise ValueError("qk_norm_rope: outputs must be contiguous bf16 [heads, l_total, 128]")
+    check(_lib.load().mq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), rows, heads, HEAD_DIM, q_weight.data_ptr(),
+                                      k_weight.data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(),
+                                      q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), row_off, l_total,
+                                      _stream_ptr()))

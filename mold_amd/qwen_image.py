@@ -35,6 +35,9 @@ Layout choices made here (the graph's values are unchanged by them):
     the joint attention and at the end of each block.
   * The residual streams stay f32; a tensor whose only consumer is a quantized
     GEMM is produced in bf16 (the GEMM rounds its input to bf16 either way).
+  * On the GPU the modulate and the q/k norm + RoPE + head split run as
+    libmoldq's fused row passes (mold_amd.fused), writing q, k, v straight
+    into the joint [heads, L, 128] bf16 buffers attention reads.
   * The text attention mask is all ones for an unpadded prompt, which makes the
     mask a no-op (:813-815 add 0 to every score), so none is applied.
 
@@ -238,7 +241,15 @@ class QwenImageStep:
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
         self.overlap = overlap
 
+    def _fused(self, x) -> bool:
+        """Use libmoldq's fused row passes (mold_amd.fused): on the GPU with bf16 GEMM inputs."""
+        import torch
+        return x.is_cuda and self.gemm_dtype == torch.bfloat16
+
     def _modulate(self, x, shift, scale):
+        if self._fused(x):
+            from .fused import adaln_modulate
+            return adaln_modulate(x, shift, scale)
         return (layer_norm(x) * (1.0 + scale) + shift).to(self.gemm_dtype)
 
     def _heads(self, y, qn, kn):
@@ -250,10 +261,17 @@ class QwenImageStep:
         k = rms_norm(y[:, 1].transpose(0, 1), self.p.dense[kn], cfg.norm_eps)
         return q, k, y[:, 2].transpose(0, 1).float()
 
-    def _txt_qkv(self, p, txt, mods, cos, sin):
+    def _txt_qkv(self, p, txt, mods, cos, sin, heads=None):
+        """The text stream's q, k, v: [H, L_txt, D] f32, or written into the joint
+        bf16 buffers `heads` = (q, k, v) at rows 0 .. L_txt - 1 (fused path)."""
         t_s1, t_c1 = mods[0], mods[1]
         import torch
         y = self.p.lin[p + "attn.add_qkv_proj"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=torch.float32)
+        if heads is not None:
+            from .fused import qk_norm_rope
+            qk_norm_rope(y, self.cfg.num_attention_heads, self.p.dense[p + "attn.norm_added_q.weight"],
+                         self.p.dense[p + "attn.norm_added_k.weight"], cos, sin, *heads, 0, self.cfg.norm_eps)
+            return None
         q, k, v = self._heads(y, p + "attn.norm_added_q.weight", p + "attn.norm_added_k.weight")
         return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
 
@@ -274,8 +292,14 @@ class QwenImageStep:
         t_mod_all = self.p.lin[p + "txt_mod.1"].forward(temb_silu)
         i_mod, t_mod = i_mod_all.chunk(6, dim=-1), t_mod_all.chunk(6, dim=-1)
         aux = self._aux(img)
+        lt = txt.shape[0]
+        fused = self._fused(img)
+        heads = None
+        if fused:
+            from .fused import new_heads
+            heads = new_heads(self.cfg.num_attention_heads, lt + img.shape[0], img.device)
         if aux is None:
-            tq, tk, tv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin)
+            tqkv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin, heads)
         else:
             # text stream on `aux`: tensors made on one stream and read on the
             # other are recorded on the reader, so the caching allocator does
@@ -283,18 +307,26 @@ class QwenImageStep:
             main = torch.cuda.current_stream(img.device)
             aux.wait_stream(main)
             with torch.cuda.stream(aux):
-                tq, tk, tv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin)
-            for t in (txt, t_mod_all):
+                tqkv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin, heads)
+            for t in (txt, t_mod_all) + (heads if heads is not None else ()):
                 t.record_stream(aux)
-            for t in (tq, tk, tv):
+            for t in (tqkv if tqkv is not None else ()):
                 t.record_stream(main)
         y = self.p.lin[p + "attn.to_qkv"].forward(self._modulate(img, i_mod[0], i_mod[1]), out_dtype=torch.float32)
-        iq, ik, iv = self._heads(y, p + "attn.norm_q.weight", p + "attn.norm_k.weight")
-        iq, ik = apply_rope(iq, img_cos, img_sin), apply_rope(ik, img_cos, img_sin)
+        if fused:
+            from .fused import qk_norm_rope
+            qk_norm_rope(y, self.cfg.num_attention_heads, self.p.dense[p + "attn.norm_q.weight"],
+                         self.p.dense[p + "attn.norm_k.weight"], img_cos, img_sin, *heads, lt, self.cfg.norm_eps)
+        else:
+            iq, ik, iv = self._heads(y, p + "attn.norm_q.weight", p + "attn.norm_k.weight")
+            iq, ik = apply_rope(iq, img_cos, img_sin), apply_rope(ik, img_cos, img_sin)
         if aux is not None:
             main.wait_stream(aux)
-        a = self.attn(torch.cat([tq, iq], dim=1), torch.cat([tk, ik], dim=1), torch.cat([tv, iv], dim=1))
-        lt = txt.shape[0]
+        if fused:
+            a = self.attn(*heads)
+        else:
+            tq, tk, tv = tqkv
+            a = self.attn(torch.cat([tq, iq], dim=1), torch.cat([tk, ik], dim=1), torch.cat([tv, iv], dim=1))
         t_att, i_att = a[:lt], a[lt:]
         if aux is None:
             txt = self._txt_tail(p, txt, t_att, t_mod)

@@ -1,0 +1,99 @@
+"""GPU tests of libmoldq's fused block glue (mq_adaln_modulate, mq_qk_norm_rope)
+against f64 torch restatements of the ops they replace:
+  modulate   LayerNorm(eps 1e-6, no affine) * (1 + scale) + shift, to bf16
+             (crates/mold-inference/src/flux/offload.rs:75-78, 283-286)
+  qk norm    x / sqrt(mean(x^2) + eps) * w for q and k per head (offload.rs:160-167, 188-201)
+  RoPE       pair (2i, 2i+1) rotated by angle i: (c x0 - s x1, s x0 + c x1) (offload.rs:56-66)
+The kernels compute in f32 and round once to bf16, so every output must lie within
+one bf16 ulp of the f64 value (half an ulp of rounding plus f32 noise), and v, a
+plain bf16 conversion, must equal torch's conversion bit for bit.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mold_amd
+from mold_amd import fused as FU
+from mold_amd._lib import MoldqError
+
+pytestmark = pytest.mark.gpu
+
+
+def _within_one_ulp(out_bf16, ref64):
+    out = out_bf16.double().cpu()
+    ref = ref64.cpu()
+    ulp = torch.clamp(ref.abs(), min=1e-30) * 2.0 ** -7
+    return bool(((out - ref).abs() <= ulp + 1e-5).all())
+
+
+@pytest.mark.parametrize("rows,cols,ld", [(1, 256, 256), (37, 3072, 3072), (300, 1024, 1280), (5, 8192, 8192)])
+def test_adaln_modulate_matches_reference(rows, cols, ld):
+    print(f"[case] adaln rows={rows} cols={cols} ld={ld}", flush=True)
+    mold_amd.load()
+    g = torch.Generator().manual_seed(rows + cols)
+    xb = (torch.randn((rows, ld), generator=g) * 3 + 0.5).cuda()
+    x = xb[:, :cols]
+    shift = torch.randn((1, cols), generator=g).cuda()
+    scale = (torch.randn((1, cols), generator=g) * 0.1).cuda()
+    out = FU.adaln_modulate(x, shift, scale)
+    torch.cuda.synchronize()
+    xd = x.double().cpu()
+    mu = xd.mean(-1, keepdim=True)
+    ref = (xd - mu) / torch.sqrt(((xd - mu) ** 2).mean(-1, keepdim=True) + 1e-6)
+    ref = ref * (1 + scale.double().cpu()) + shift.double().cpu()
+    assert out.dtype == torch.bfloat16 and out.shape == (rows, cols)
+    assert _within_one_ulp(out, ref)
+
+
+@pytest.mark.parametrize("rows,heads,extra,row_off,l_total", [(37, 3, 64, 5, 50), (512, 24, 0, 0, 512),
+                                                              (64, 2, 12288 - 768, 100, 164)])
+def test_qk_norm_rope_matches_reference(rows, heads, extra, row_off, l_total):
+    print(f"[case] qk_norm_rope rows={rows} heads={heads} off={row_off}", flush=True)
+    mold_amd.load()
+    g = torch.Generator().manual_seed(rows * heads)
+    d = 128
+    ld = 3 * heads * d + extra
+    y = (torch.randn((rows, ld), generator=g) * 2).cuda()
+    qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
+    kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
+    ang = torch.rand((rows, d // 2), generator=g, dtype=torch.float64) * 50
+    cos, sin = torch.cos(ang).float().cuda(), torch.sin(ang).float().cuda()
+    q, k, v = FU.new_heads(heads, l_total, "cuda")
+    for t in (q, k, v):
+        t.fill_(7.0)
+    FU.qk_norm_rope(y, heads, qw, kw, cos, sin, q, k, v, row_off)
+    torch.cuda.synchronize()
+    yd = y.double().cpu()[:, :3 * heads * d].reshape(rows, 3, heads, d).permute(1, 2, 0, 3)  # [3, H, L, D]
+    c, s = cos.double().cpu(), sin.double().cpu()
+
+    def norm_rope(x, w):
+        x = x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-6) * w.double().cpu()
+        x0, x1 = x[..., 0::2], x[..., 1::2]
+        return torch.stack([c * x0 - s * x1, s * x0 + c * x1], dim=-1).reshape(x.shape)
+
+    sl = slice(row_off, row_off + rows)
+    assert _within_one_ulp(q[:, sl], norm_rope(yd[0], qw))
+    assert _within_one_ulp(k[:, sl], norm_rope(yd[1], kw))
+    vref = y[:, 2 * heads * d:3 * heads * d].reshape(rows, heads, d).transpose(0, 1).to(torch.bfloat16)
+    assert torch.equal(v[:, sl].view(torch.int16), vref.view(torch.int16))
+    # rows outside the segment are untouched
+    assert bool((q[:, :row_off] == 7.0).all()) and bool((q[:, row_off + rows:] == 7.0).all())
+
+
+def test_glue_errors_are_reported():
+    mold_amd.load()
+    y = torch.zeros((4, 3 * 128), device="cuda")
+    cs = torch.zeros((4, 64), device="cuda")
+    w = torch.ones(128, dtype=torch.bfloat16, device="cuda")
+    q, k, v = FU.new_heads(1, 4, "cuda")
+    lib = mold_amd.load()
+    rc = lib.mq_qk_norm_rope(y.data_ptr(), y.stride(0), 4, 1, 64, w.data_ptr(), w.data_ptr(), 1e-6, cs.data_ptr(),
+                             cs.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, 4, None)
+    assert rc == -1 and b"head_dim" in lib.mq_last_error()
+    with pytest.raises(MoldqError):   # row range past the joint sequence
+        FU.qk_norm_rope(y, 1, w, w, cs, cs, q, k, v, 2)
+    x = torch.zeros((2, 6), device="cuda")
+    with pytest.raises(ValueError):
+        FU.adaln_modulate(x, torch.zeros(5, device="cuda"), torch.zeros(5, device="cuda"))
+    with pytest.raises(MoldqError):   # cols not a multiple of 4
+        FU.adaln_modulate(x, torch.zeros(6, device="cuda"), torch.zeros(6, device="cuda"))
