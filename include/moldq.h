@@ -146,6 +146,16 @@ int mq_qk_norm_rope(const float *qkv, int64_t ld, int64_t rows, int heads, int h
                     const void *k_weight, float eps, const float *cos_table, const float *sin_table, void *q_out,
                     void *k_out, void *v_out, int64_t row_off, int64_t l_total, void *stream);
 
+/* The DiT blocks' gated residual update through one quantized linear:
+ * y[m, :n] += gate[:n] * (x[m, :k] . W^T + bias), y f32 (row stride ldy),
+ * updated in place; gate f32 [n]; bias f32 [n] or NULL; x F32 or BF16.  Fuses
+ * `x + gate * linear(h)` of crates/mold-inference/src/flux/offload.rs:301-305,
+ * 314-321, 389-391 and crates/mold-inference/src/qwen_image/
+ * quantized_transformer.rs:937-938, 954-958 into the GEMM's epilogue (every m
+ * takes the GEMM kernel). */
+int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
+                         float *y, int64_t ldy, const float *bias, const float *gate, void *stream);
+
 /* --- GGUF v2/v3 reader (candle gguf_file::Content::read, used at
  *     crates/mold-inference/src/flux/pipeline.rs:286-287). ------------------- */
 int mq_gguf_open(const char *path, mq_gguf **out);

@@ -123,6 +123,34 @@ int ensure_scratch(mq_ctx *ctx, size_t bytes) {
 
 WView view_of(const mq_qtensor *w) { return make_view(w->data, w->geo); }
 
+// GEMM: stage activations as bf16 [m, kp] (kp multiple of 64, zero padded)
+// unless bf16 x can be read in place, then the fused dequant-MFMA kernel.
+int run_gemm(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
+             int y_dtype, int64_t ldy, const float *bias, const float *gate, int act, hipStream_t s) {
+  const WView wv = view_of(w);
+  const int64_t n = w->n, k = w->k;
+  const int64_t kp = (k + 63) / 64 * 64;
+  const __bf16 *a = nullptr;
+  int64_t lda = 0;
+  const bool direct = x_dtype == MQ_BF16 && k == kp && (ldx % 8) == 0 &&
+                      (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (direct) {
+    a = static_cast<const __bf16 *>(x);
+    lda = ldx;
+  } else {
+    int rc = ensure_scratch(ctx, (size_t)m * kp * sizeof(__bf16));
+    if (rc) return rc;
+    __bf16 *st = static_cast<__bf16 *>(ctx->scratch);
+    hipError_t e = launch_stage_bf16(x, x_dtype, m, k, ldx, st, kp, s);
+    if (e != hipSuccess) return hip_fail(e, "stage activations");
+    a = st;
+    lda = kp;
+  }
+  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, s);
+  if (e != hipSuccess) return hip_fail(e, "gemm launch");
+  return MQ_OK;
+}
+
 }  // namespace
 
 namespace mq {
@@ -379,27 +407,22 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
     return MQ_OK;
   }
 
-  // GEMM: stage activations as bf16 [m, kp] (kp multiple of 64, zero padded)
-  const int64_t kp = (k + 63) / 64 * 64;
-  const __bf16 *a = nullptr;
-  int64_t lda = 0;
-  const bool direct = x_dtype == MQ_BF16 && k == kp && (ldx % 8) == 0 &&
-                      (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  if (direct) {
-    a = static_cast<const __bf16 *>(x);
-    lda = ldx;
-  } else {
-    int rc = ensure_scratch(ctx, (size_t)m * kp * sizeof(__bf16));
-    if (rc) return rc;
-    __bf16 *st = static_cast<__bf16 *>(ctx->scratch);
-    hipError_t e = launch_stage_bf16(x, x_dtype, m, k, ldx, st, kp, s);
-    if (e != hipSuccess) return hip_fail(e, "stage activations");
-    a = st;
-    lda = kp;
-  }
-  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, act, s);
-  if (e != hipSuccess) return hip_fail(e, "gemm launch");
-  return MQ_OK;
+  return run_gemm(ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
+}
+
+int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
+                         float *y, int64_t ldy, const float *bias, const float *gate, void *stream) {
+  if (!ctx || !w) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL ctx or weight");
+  if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: m=%lld < 0", (long long)m);
+  if (m == 0) return MQ_OK;
+  if (!x || !y || !gate) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL x, y or gate");
+  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
+    return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: x dtype %d must be F32 or BF16", x_dtype);
+  if (ldx < w->k) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: ldx=%lld < k=%lld", (long long)ldx, (long long)w->k);
+  if (ldy < w->n) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: ldy=%lld < n=%lld", (long long)ldy, (long long)w->n);
+  DeviceGuard g(ctx->device);
+  // every m takes the GEMM kernel: its epilogue holds the gated update
+  return run_gemm(ctx, w, x, x_dtype, m, ldx, y, MQ_F32, ldy, bias, gate, MQ_ACT_NONE, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

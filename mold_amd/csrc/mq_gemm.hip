@@ -21,6 +21,7 @@
 // the per-type chunk order TT::chunk(s, h) in gemm_fast_kernel; the A operand
 // reads the same runs from LDS, so the K order inside a step is a permutation
 // shared by both operands.
+#include <type_traits>
 #include <utility>
 
 #include "mq_bfrag.h"
@@ -59,10 +60,22 @@ __device__ __forceinline__ void store_out<float>(float *p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_out<__bf16>(__bf16 *p, float v) { *p = (__bf16)v; }
 
+// y = v, or with a gate (f32 output only) the gated residual update
+// y = r + g * v of the DiT blocks, r read through its own pointer `res`
+// (the same buffer as y): loads of r never wait behind stores of y.
+template <typename OUT>
+__device__ __forceinline__ void store_epi(OUT *p, const float *r, float v, const float *gate, float g) {
+  if constexpr (std::is_same_v<OUT, float>) {
+    if (gate) v = __builtin_fmaf(g, v, *r);
+  }
+  store_out<OUT>(p, v);
+}
+
 template <int TYPE, typename OUT>
 __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m,
-    int64_t lda, OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act, int tiles_m,
+    int64_t lda, OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias,
+    const float *__restrict__ gate, const float *__restrict__ res, int act, int tiles_m,
     int tiles_n) {
   constexpr TypeInfo ti = type_info(TYPE);
   __shared__ uint4 lds[2][kBM * kBK / 8];  // 2 x 32 KiB, row = 8 chunks of 16 B
@@ -170,12 +183,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
     const int64_t col = wt_raw * kRowTile + nb * 32 + l32;
     if (col >= n) continue;
     const float bv = bias ? bias[col] : 0.f;
+    const float g = gate ? gate[col] : 0.f;
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + mb * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        if (row < m) store_out<OUT>(y + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act));
+        if (row < m)
+          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act), gate, g);
       }
     }
   }
@@ -225,7 +240,8 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
 template <int TYPE, typename OUT>
 __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
-    OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act, int tiles_m, int tiles_n) {
+    OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate,
+    const float *__restrict__ res, int act, int tiles_m, int tiles_n) {
   using TT = bfrag::T<TYPE>;
   constexpr int kSteps = TT::kUnitK / kBK;
   // VALU instructions placed after each pair of MFMAs (the decode work per
@@ -378,11 +394,37 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     for (int nb = 0; nb < 2; ++nb) {
       const float bv = bias ? bias[col0 + nb * 32] : 0.f;
       OUT *yc = y + row0 * ldy + col0 + nb * 32;
+      if constexpr (std::is_same_v<OUT, float>) {
+        if (gate) {
+          // residual rows of 32-row block mb + 1 are loaded before block mb is
+          // stored: one memory latency per tile column, not one per element
+          const float g = gate[col0 + nb * 32];
+          const float *rc = res + row0 * ldy + col0 + nb * 32;
+          float r[2][16];
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
+          for (int e = 0; e < 16; ++e) r[0][e] = rc[(8 * (e >> 2) + (e & 3)) * ldy];
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][nb][e] + bv);
+          for (int mb = 0; mb < 8; ++mb) {
+            if (mb + 1 < 8) {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) r[(mb + 1) & 1][e] = rc[((mb + 1) * 32 + 8 * (e >> 2) + (e & 3)) * ldy];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              yc[(mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy] = __builtin_fmaf(g, acc[mb][nb][e] + bv, r[mb & 1][e]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          continue;
+        }
+      }
+      {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][nb][e] + bv);
+      }
     }
     return;
   }
@@ -391,12 +433,41 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     const int64_t col = col0 + nb * 32;
     if (col >= n) continue;
     const float bv = bias ? bias[col] : 0.f;
+    const float g = gate ? gate[col] : 0.f;
+    if constexpr (std::is_same_v<OUT, float>) {
+      if (gate) {
+        // as the full-tile path: block mb + 1's residual rows loaded before
+        // block mb is stored; rows past m are neither read nor written
+        float r[2][16];
+        auto load_block = [&](int mb, float *dst) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
+            dst[e] = row < m ? res[row * ldy + col] : 0.f;
+          }
+        };
+        load_block(0, r[0]);
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) {
+          if (mb + 1 < 8) load_block(mb + 1, r[(mb + 1) & 1]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
+            if (row < m) y[row * ldy + col] = __builtin_fmaf(g, apply_act(acc[mb][nb][e] + bv, act), r[mb & 1][e]);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
-        if (row < m) store_out<OUT>(y + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act));
+        if (row < m)
+          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act), gate, g);
       }
     }
   }
@@ -404,44 +475,45 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
 
 template <int T>
 hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
-                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
-                            hipStream_t stream) {
+                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
+                            int act, hipStream_t stream) {
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const int grid = tiles_m * tiles_n;
   // fast path: whole 256-wide units, 16-byte aligned rows, and element
   // offsets of x that fit the kernel's 32-bit row offsets
   const bool fast = (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
+  const float *res = gate ? static_cast<const float *>(y) : nullptr;  // the gated update reads y, then writes it
   if (fast) {
     if (y_type == F32)
       hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                         ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
+                         ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
     else
       hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                         ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
+                         ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
   } else if (y_type == F32) {
     hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
-                       a, m, lda, static_cast<float *>(y), ldy, bias, act, tiles_m, tiles_n);
+                       a, m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
   } else {
     hipLaunchKernelGGL((gemm_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
-                       a, m, lda, static_cast<__bf16 *>(y), ldy, bias, act, tiles_m, tiles_n);
+                       a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
   }
   return hipGetLastError();
 }
 
 template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64_t, int64_t, const __bf16 *,
-                                                   int64_t, int64_t, void *, int, int64_t, const float *, int,
-                                                   hipStream_t);
+                                                   int64_t, int64_t, void *, int, int64_t, const float *,
+                                                   const float *, int, hipStream_t);
 
 #else  // the type dispatcher
 
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,
-                       int64_t m, int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
-                       hipStream_t stream) {
+                       int64_t m, int64_t lda, void *y, int y_type, int64_t ldy, const float *bias,
+                       const float *gate, int act, hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
   hipError_t err = hipErrorInvalidValue;
   dispatch_type(type, [&]<int T>() {
-    err = launch_gemm_type<T>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, act, stream);
+    err = launch_gemm_type<T>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, stream);
   });
   return err;
 }

@@ -34,15 +34,17 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const flo
                        float *partial, int cus, hipStream_t stream);
 
 // Fused dequant -> LDS -> bf16 MFMA GEMM.  a is bf16 [m, lda] with lda a
-// multiple of 64 covering ceil(k/64)*64 zero-padded columns.
+// multiple of 64 covering ceil(k/64)*64 zero-padded columns.  With `gate`
+// (f32 [n], f32 y only) the output is the gated residual update
+// y = y + gate * act(a . W^T + bias); without it y = act(a . W^T + bias).
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w,
                        const __bf16 *a, int64_t m, int64_t lda, void *y, int y_type, int64_t ldy,
-                       const float *bias, int act, hipStream_t stream);
+                       const float *bias, const float *gate, int act, hipStream_t stream);
 // One weight type's launcher (instantiated in its own translation unit).
 template <int T>
 hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
-                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, int act,
-                            hipStream_t stream);
+                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
+                            int act, hipStream_t stream);
 
 // Epilogue activation (GELU with the tanh approximation, as candle's gelu()).
 __device__ __forceinline__ float apply_act(float v, int act) {

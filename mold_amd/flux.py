@@ -25,8 +25,9 @@ Activations are f32, as in mold's quantized FLUX path
 (crates/mold-inference/src/flux/pipeline.rs:1524,1639-1647).  MI355X
 choices, each documented where it is made: on the GPU the modulate and the
 q/k norm + RoPE + head split run as libmoldq's fused row passes
-(mold_amd.fused), one HBM pass each instead of a dozen elementwise ops; a
-tensor whose only consumer is a quantized GEMM is produced directly in bf16
+(mold_amd.fused), one HBM pass each instead of a dozen elementwise ops, and
+each gated residual update x + gate * linear(h) is the GEMM's epilogue
+(Linear.gated_add, updating x in place); a tensor whose only consumer is a quantized GEMM is produced directly in bf16
 (the GEMM rounds its input to bf16 with round-to-nearest-even either way, so
 the f32 -> bf16 staging pass disappears); and attention runs in bf16 with f32
 softmax accumulation (PyTorch's fused attention) rather than as three f32 ops.
@@ -270,6 +271,7 @@ class FluxStep:
         self.attn = attn
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
         self.fused = fused
+        self.gated_epilogue = True
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused) for the modulate and the
@@ -298,6 +300,14 @@ class FluxStep:
             from .fused import adaln_modulate
             return adaln_modulate(x, shift, scale)
         return (layer_norm(x) * (1.0 + scale) + shift).to(self.gemm_dtype)
+
+    def _gated(self, name, h, gate, res):
+        """res + gate * lin(h): on the fused path with `gated_epilogue` the GEMM's
+        epilogue updates res in place (Linear.gated_add); otherwise a new tensor."""
+        import torch
+        if self._fused(res) and self.gated_epilogue:
+            return self.p.lin[name].gated_add(h, gate, res)
+        return res + gate * self.p.lin[name].forward(h, out_dtype=torch.float32)
 
     def _heads_fused(self, segments, cos, sin):
         """q, k, v bf16 [H, L, D] of the joint sequence from (qkv f32 [L_seg, >= 3h],
@@ -337,14 +347,14 @@ class FluxStep:
         a = self.attn(q, k, v)
         lt = txt.shape[0]
         t_att, i_att = a[:lt], a[lt:]
-        img = img + i_g1 * self.p.lin[p + "img_attn.proj"].forward(i_att, out_dtype=torch.float32)
+        img = self._gated(p + "img_attn.proj", i_att, i_g1, img)
         h = self.p.lin[p + "img_mlp.0"].forward(self._modulate(img, i_s2, i_c2), act=ACT_GELU_TANH,
                                                out_dtype=self.gemm_dtype)
-        img = img + i_g2 * self.p.lin[p + "img_mlp.2"].forward(h, out_dtype=torch.float32)
-        txt = txt + t_g1 * self.p.lin[p + "txt_attn.proj"].forward(t_att, out_dtype=torch.float32)
+        img = self._gated(p + "img_mlp.2", h, i_g2, img)
+        txt = self._gated(p + "txt_attn.proj", t_att, t_g1, txt)
         h = self.p.lin[p + "txt_mlp.0"].forward(self._modulate(txt, t_s2, t_c2), act=ACT_GELU_TANH,
                                                out_dtype=self.gemm_dtype)
-        txt = txt + t_g2 * self.p.lin[p + "txt_mlp.2"].forward(h, out_dtype=torch.float32)
+        txt = self._gated(p + "txt_mlp.2", h, t_g2, txt)
         return img, txt
 
     def single_block(self, i, x, vec, cos, sin):
@@ -365,7 +375,7 @@ class FluxStep:
         cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
         cat[:, :h] = a
         cat[:, h:] = gelu_tanh(y[:, 3 * h:])
-        return x + gate * self.p.lin[p + "linear2"].forward(cat, out_dtype=torch.float32)
+        return self._gated(p + "linear2", cat, gate, x)
 
     def stems(self, img, txt, t, guidance, y):
         import torch

@@ -255,4 +255,27 @@ class Linear:
     def forward(self, x, act: int = ACT_NONE, out_dtype=None, stream=None):
         return self.matmul.forward(x, bias=self.bias, act=act, out_dtype=out_dtype, stream=stream)
 
+    def gated_add(self, x, gate, residual, stream=None):
+        """residual += gate * forward(x), in place, fused into the GEMM epilogue
+        (mq_qmatmul_gated_add); residual f32 [m, n] with unit column stride,
+        gate f32 with n elements.  Returns residual."""
+        torch = _torch()
+        qt = self.matmul.w
+        n, k = qt.shape
+        x2 = x.reshape(-1, k)
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        g = gate.reshape(-1)
+        if residual.dtype != torch.float32 or residual.dim() != 2 or residual.stride(1) != 1 \
+                or tuple(residual.shape) != (x2.shape[0], n):
+            raise ValueError("gated_add: residual must be f32 [m, n] with unit column stride")
+        if g.dtype != torch.float32 or not g.is_contiguous() or g.numel() != n:
+            raise ValueError("gated_add: gate must be contiguous f32 with n elements")
+        b = self.bias
+        check(_lib.load().mq_qmatmul_gated_add(qt.device.handle, qt.handle, x2.data_ptr(), _dtype_code(x2.dtype),
+                                               x2.shape[0], x2.stride(0), residual.data_ptr(), residual.stride(0),
+                                               b.data_ptr() if b is not None else None, g.data_ptr(),
+                                               _stream_ptr(stream)))
+        return residual
+
     __call__ = forward

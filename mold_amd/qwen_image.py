@@ -37,7 +37,9 @@ Layout choices made here (the graph's values are unchanged by them):
     GEMM is produced in bf16 (the GEMM rounds its input to bf16 either way).
   * On the GPU the modulate and the q/k norm + RoPE + head split run as
     libmoldq's fused row passes (mold_amd.fused), writing q, k, v straight
-    into the joint [heads, L, 128] bf16 buffers attention reads.
+    into the joint [heads, L, 128] bf16 buffers attention reads, and each
+    gated residual update x + gate * linear(h) is the GEMM's epilogue
+    (Linear.gated_add, updating x in place).
   * The text attention mask is all ones for an unpadded prompt, which makes the
     mask a no-op (:813-815 add 0 to every score), so none is applied.
 
@@ -240,6 +242,7 @@ class QwenImageStep:
         self.attn = attn
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
         self.overlap = overlap
+        self.gated_epilogue = True
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused): on the GPU with bf16 GEMM inputs."""
@@ -275,13 +278,20 @@ class QwenImageStep:
         q, k, v = self._heads(y, p + "attn.norm_added_q.weight", p + "attn.norm_added_k.weight")
         return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
 
-    def _txt_tail(self, p, txt, t_att, mods):
+    def _gated(self, name, h, gate, res):
+        """res + gate * lin(h): on the fused path with `gated_epilogue` the GEMM's
+        epilogue updates res in place (Linear.gated_add); otherwise a new tensor."""
         import torch
+        if self._fused(res) and self.gated_epilogue:
+            return self.p.lin[name].gated_add(h, gate, res)
+        return res + gate * self.p.lin[name].forward(h, out_dtype=torch.float32)
+
+    def _txt_tail(self, p, txt, t_att, mods):
         _, _, t_g1, t_s2, t_c2, t_g2 = mods
-        txt = txt + t_g1 * self.p.lin[p + "attn.to_add_out"].forward(t_att, out_dtype=torch.float32)
+        txt = self._gated(p + "attn.to_add_out", t_att, t_g1, txt)
         h = self.p.lin[p + "txt_mlp.net.0.proj"].forward(self._modulate(txt, t_s2, t_c2), act=ACT_GELU_TANH,
                                                         out_dtype=self.gemm_dtype)
-        return txt + t_g2 * self.p.lin[p + "txt_mlp.net.2"].forward(h, out_dtype=torch.float32)
+        return self._gated(p + "txt_mlp.net.2", h, t_g2, txt)
 
     def block(self, i, img, txt, temb_silu, rope):
         """QwenImageTransformerBlock.forward (:856-960)."""
@@ -338,10 +348,10 @@ class QwenImageStep:
                 t.record_stream(aux)
             txt = txt_new
         _, _, i_g1, i_s2, i_c2, i_g2 = i_mod
-        img = img + i_g1 * self.p.lin[p + "attn.to_out.0"].forward(i_att, out_dtype=torch.float32)
+        img = self._gated(p + "attn.to_out.0", i_att, i_g1, img)
         h = self.p.lin[p + "img_mlp.net.0.proj"].forward(self._modulate(img, i_s2, i_c2), act=ACT_GELU_TANH,
                                                         out_dtype=self.gemm_dtype)
-        img = img + i_g2 * self.p.lin[p + "img_mlp.net.2"].forward(h, out_dtype=torch.float32)
+        img = self._gated(p + "img_mlp.net.2", h, i_g2, img)
         if aux is not None:
             main.wait_stream(aux)
             txt.record_stream(main)

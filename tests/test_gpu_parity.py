@@ -309,6 +309,36 @@ def test_gemm_bias_gelu_bf16_and_strides(dev, torch):
     assert torch.all(out[:, n:] == 7.0)
 
 
+@pytest.mark.parametrize("m,n,k,tname,xbf16", [(300, 200, 512, "Q4_K", False), (4, 128, 256, "Q8_0", True),
+                                                (513, 320, 768, "Q6_K", False), (256, 3072, 3072, "Q2_K", True)])
+def test_qmatmul_gated_add(dev, torch, m, n, k, tname, xbf16):
+    """mq_qmatmul_gated_add: residual += gate * (x . W^T + bias) in the GEMM epilogue,
+    on a strided residual; the update must meet the GEMM bar against the f64 oracle and
+    leave the columns past n untouched."""
+    t = GgmlDType[tname]
+    _say(f"gated add {tname} m={m} n={n} k={k} bf16={xbf16}")
+    blocks = _weights(int(t), n, k, seed=m + n)
+    lin = mold_amd.Linear(QTensor.from_blocks(dev, t, (n, k), blocks),
+                          torch.from_numpy((np.random.default_rng(1).standard_normal(n) * 0.1).astype(np.float32)).cuda())
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    if xbf16:
+        xt = xt.to(torch.bfloat16)
+        x = xt.float().cpu().numpy()
+    gate = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+    res0 = torch.from_numpy(rng.standard_normal((m, n + 16)).astype(np.float32)).cuda()
+    res = res0.clone()
+    out = lin.gated_add(xt, gate, res[:, :n])
+    torch.cuda.synchronize()
+    assert out.data_ptr() == res.data_ptr()
+    ref = (O.matmul_f64(int(t), x, blocks, n, k) + lin.bias.cpu().numpy()) * gate.cpu().numpy()
+    delta = (res[:, :n] - res0[:, :n]).cpu().numpy()
+    assert np.isfinite(delta).all()
+    assert O.rel_l2(delta, ref) <= GEMM_TOL
+    assert torch.equal(res[:, n:], res0[:, n:])
+
+
 def test_gemm_and_gemv_deterministic(dev, torch):
     t, n, k = GgmlDType.Q4_K, 512, 1536
     _say("determinism")
