@@ -212,6 +212,20 @@ def silu(x):
     return torch.nn.functional.silu(x)
 
 
+_AUX: Dict[int, object] = {}
+
+
+def aux_stream(device):
+    """One extra stream per device (default priority) for a block's second token stream."""
+    import torch
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _AUX.get(idx)
+    if s is None:
+        s = torch.cuda.Stream(device=idx)
+        _AUX[idx] = s
+    return s
+
+
 ATTENTION_BACKEND = {"name": None}
 
 
@@ -329,21 +343,15 @@ class FluxStep:
         t_s1, t_c1, t_g1, t_s2, t_c2, t_g2 = self._mod(p + "txt_mod.lin", vec, 6)
         import torch
         if self._fused(img):
-            f32 = torch.float32
-            ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=f32)
-            iy = self.p.lin[p + "img_attn.qkv"].forward(self._modulate(img, i_s1, i_c1), out_dtype=f32)
-            q, k, v = self._heads_fused(
-                [(ty, p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale"),
-                 (iy, p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")], cos, sin)
-            del ty, iy
-        else:
-            iq, ik, iv = self._qkv(p + "img_attn.", self._modulate(img, i_s1, i_c1),
-                                   p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")
-            tq, tk, tv = self._qkv(p + "txt_attn.", self._modulate(txt, t_s1, t_c1),
-                                   p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale")
-            q = apply_rope(torch.cat([tq, iq], dim=1), cos, sin)
-            k = apply_rope(torch.cat([tk, ik], dim=1), cos, sin)
-            v = torch.cat([tv, iv], dim=1)
+            return self._double_block_fused(p, img, txt, cos, sin, (i_s1, i_c1, i_g1, i_s2, i_c2, i_g2),
+                                            (t_s1, t_c1, t_g1, t_s2, t_c2, t_g2))
+        iq, ik, iv = self._qkv(p + "img_attn.", self._modulate(img, i_s1, i_c1),
+                               p + "img_attn.norm.query_norm.scale", p + "img_attn.norm.key_norm.scale")
+        tq, tk, tv = self._qkv(p + "txt_attn.", self._modulate(txt, t_s1, t_c1),
+                               p + "txt_attn.norm.query_norm.scale", p + "txt_attn.norm.key_norm.scale")
+        q = apply_rope(torch.cat([tq, iq], dim=1), cos, sin)
+        k = apply_rope(torch.cat([tk, ik], dim=1), cos, sin)
+        v = torch.cat([tv, iv], dim=1)
         a = self.attn(q, k, v)
         lt = txt.shape[0]
         t_att, i_att = a[:lt], a[lt:]
@@ -355,6 +363,47 @@ class FluxStep:
         h = self.p.lin[p + "txt_mlp.0"].forward(self._modulate(txt, t_s2, t_c2), act=ACT_GELU_TANH,
                                                out_dtype=self.gemm_dtype)
         txt = self._gated(p + "txt_mlp.2", h, t_g2, txt)
+        return img, txt
+
+    def _double_block_fused(self, p, img, txt, cos, sin, im, tm):
+        """The double block on the GPU: the text stream's linears (M = 512) run on a
+        second HIP stream while the image stream's (M = 4096) fill the rest of the
+        chip, joined before attention and at the end.  Tensors made on one stream and
+        read on the other are recorded on the reader (caching-allocator safety).  The
+        text-side linears take bf16 activations read in place, so they use none of the
+        library context's shared staging scratch."""
+        import torch
+        from .fused import new_heads, qk_norm_rope
+        f32 = torch.float32
+        lt, H = txt.shape[0], self.cfg.num_heads
+        q, k, v = new_heads(H, lt + img.shape[0], img.device)
+        main = torch.cuda.current_stream(img.device)
+        aux = aux_stream(img.device)
+        aux.wait_stream(main)
+        with torch.cuda.stream(aux):
+            ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, tm[0], tm[1]), out_dtype=f32)
+            qk_norm_rope(ty, H, self.p.dense[p + "txt_attn.norm.query_norm.scale"],
+                         self.p.dense[p + "txt_attn.norm.key_norm.scale"], cos[:lt], sin[:lt], q, k, v, 0)
+        for t in (txt, tm[0], q, k, v, cos, sin):
+            t.record_stream(aux)
+        iy = self.p.lin[p + "img_attn.qkv"].forward(self._modulate(img, im[0], im[1]), out_dtype=f32)
+        qk_norm_rope(iy, H, self.p.dense[p + "img_attn.norm.query_norm.scale"],
+                     self.p.dense[p + "img_attn.norm.key_norm.scale"], cos[lt:], sin[lt:], q, k, v, lt)
+        main.wait_stream(aux)
+        a = self.attn(q, k, v)
+        t_att, i_att = a[:lt], a[lt:]
+        aux.wait_stream(main)
+        with torch.cuda.stream(aux):
+            txt = self._gated(p + "txt_attn.proj", t_att, tm[2], txt)
+            h = self.p.lin[p + "txt_mlp.0"].forward(self._modulate(txt, tm[3], tm[4]), act=ACT_GELU_TANH,
+                                                   out_dtype=self.gemm_dtype)
+            txt = self._gated(p + "txt_mlp.2", h, tm[5], txt)
+        a.record_stream(aux)
+        img = self._gated(p + "img_attn.proj", i_att, im[2], img)
+        h = self.p.lin[p + "img_mlp.0"].forward(self._modulate(img, im[3], im[4]), act=ACT_GELU_TANH,
+                                               out_dtype=self.gemm_dtype)
+        img = self._gated(p + "img_mlp.2", h, im[5], img)
+        main.wait_stream(aux)
         return img, txt
 
     def single_block(self, i, x, vec, cos, sin):

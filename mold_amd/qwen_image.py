@@ -55,7 +55,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
-from .flux import apply_rope, attention_bf16, gelu_tanh, layer_norm, silu
+from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, silu
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
 MAX_PERIOD = 10000.0
@@ -215,19 +215,6 @@ def rope_tables(cfg: QwenConfig, frames: int, height: int, width: int, txt_len: 
     return (torch.cos(img).float(), torch.sin(img).float(), torch.cos(txt).float(), torch.sin(txt).float())
 
 
-def _aux_stream(device_index: int):
-    """One extra default-priority stream per device for the text-stream linears."""
-    import torch
-    s = _AUX.get(device_index)
-    if s is None:
-        s = torch.cuda.Stream(device=device_index)
-        _AUX[device_index] = s
-    return s
-
-
-_AUX: Dict[int, object] = {}
-
-
 class QwenImageStep:
     """One denoising-step forward of the Qwen-Image transformer (batch 1).
 
@@ -365,7 +352,7 @@ class QwenImageStep:
         use = self.overlap if self.overlap is not None else x.is_cuda
         if not use or not x.is_cuda or self.gemm_dtype != torch.bfloat16:
             return None
-        return _aux_stream(x.device.index if x.device.index is not None else torch.cuda.current_device())
+        return aux_stream(x.device)
 
     def stems(self, img, txt, t):
         import torch
