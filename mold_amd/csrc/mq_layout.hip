@@ -143,10 +143,39 @@ __global__ void stage_bf16_kernel(const IN *__restrict__ x, int64_t m, int64_t k
   }
 }
 
+// f32 rows with k a multiple of 8, 4-aligned row stride, 16-byte aligned x:
+// two 16-byte loads and one 16-byte store per thread, a 2-D grid (column
+// groups x rows, rows strided by gridDim.y), no divides.
+__global__ __launch_bounds__(256) void stage_bf16_vec_kernel(const float4 *__restrict__ x, int64_t m, int64_t k,
+                                                             int64_t ldx4, bf16x8 *__restrict__ out, int64_t kp) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 8-column group
+  if (g >= (kp >> 3)) return;
+  for (int64_t row = blockIdx.y; row < m; row += gridDim.y) {
+    bf16x8 r;
+    if (8 * g < k) {
+      const float4 a = x[row * ldx4 + 2 * g], b = x[row * ldx4 + 2 * g + 1];
+      r[0] = (__bf16)a.x; r[1] = (__bf16)a.y; r[2] = (__bf16)a.z; r[3] = (__bf16)a.w;
+      r[4] = (__bf16)b.x; r[5] = (__bf16)b.y; r[6] = (__bf16)b.z; r[7] = (__bf16)b.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] = (__bf16)0.0f;
+    }
+    out[row * (kp >> 3) + g] = r;
+  }
+}
+
 hipError_t launch_stage_bf16(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, __bf16 *out,
                              int64_t kp, hipStream_t stream) {
   const int64_t total = m * (kp >> 3);
   if (total == 0) return hipSuccess;
+  if (x_type == F32 && k % 8 == 0 && ldx % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const int64_t groups = kp >> 3;
+    const unsigned gx = (unsigned)((groups + 255) / 256);
+    const unsigned gy = (unsigned)(m < 65535 ? m : 65535);
+    hipLaunchKernelGGL(stage_bf16_vec_kernel, dim3(gx, gy), dim3(256), 0, stream, static_cast<const float4 *>(x), m,
+                       k, ldx / 4, reinterpret_cast<bf16x8 *>(out), kp);
+    return hipGetLastError();
+  }
   const int threads = 256;
   const int64_t want = (total + threads - 1) / threads;
   const int blocks = (int)(want < 262144 ? want : 262144);
