@@ -22,6 +22,16 @@ struct mq_ctx {
   // Scratch: activation staging and GEMV partial sums.
   void *scratch = nullptr;
   size_t scratch_size = 0;
+  // GEMM tail-tile partial sums, one buffer per stream (so GEMMs with
+  // in-place bf16 x may run concurrently on different streams).
+  struct StreamBuf {
+    hipStream_t stream = nullptr;
+    void *p = nullptr;
+    size_t size = 0;
+  };
+  static constexpr int kTailStreams = 4;
+  StreamBuf tail[kTailStreams];
+  int tail_used = 0;
 };
 
 struct mq_qtensor {
@@ -123,6 +133,35 @@ int ensure_scratch(mq_ctx *ctx, size_t bytes) {
 
 WView view_of(const mq_qtensor *w) { return make_view(w->data, w->geo); }
 
+// The stream's tail-partial buffer of at least `bytes`, or NULL when the
+// context already serves kTailStreams other streams (the GEMM then runs every
+// tile whole) or the allocation fails.
+float *tail_buffer(mq_ctx *ctx, hipStream_t s, size_t bytes) {
+  mq_ctx::StreamBuf *b = nullptr;
+  for (int i = 0; i < ctx->tail_used; ++i)
+    if (ctx->tail[i].stream == s) b = &ctx->tail[i];
+  if (!b) {
+    if (ctx->tail_used == mq_ctx::kTailStreams) return nullptr;
+    b = &ctx->tail[ctx->tail_used++];
+    b->stream = s;
+  }
+  if (b->size < bytes) {
+    if (b->p) {
+      if (hipStreamSynchronize(s) != hipSuccess) return nullptr;  // earlier work on s may still read it
+      (void)hipFree(b->p);
+      b->p = nullptr;
+      b->size = 0;
+    }
+    const size_t sz = (bytes + (1 << 20) - 1) & ~size_t((1 << 20) - 1);
+    if (hipMalloc(&b->p, sz) != hipSuccess) {
+      b->p = nullptr;
+      return nullptr;
+    }
+    b->size = sz;
+  }
+  return static_cast<float *>(b->p);
+}
+
 // GEMM: stage activations as bf16 [m, kp] (kp multiple of 64, zero padded)
 // unless bf16 x can be read in place, then the fused dequant-MFMA kernel.
 int run_gemm(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
@@ -146,7 +185,11 @@ int run_gemm(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64
     a = st;
     lda = kp;
   }
-  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, s);
+  GemmTail tail = gemm_tail_plan(m, n, k, ctx->cu_count);
+  float *partial = nullptr;
+  if (tail.kparts > 1 && gemm_fast_ok(m, k, lda)) partial = tail_buffer(ctx, s, gemm_tail_bytes(tail, m, n));
+  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, tail,
+                             partial, s);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");
   return MQ_OK;
 }
@@ -202,6 +245,8 @@ void mq_ctx_destroy(mq_ctx *ctx) {
   DeviceGuard g(ctx->device);
   (void)hipDeviceSynchronize();
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  for (int i = 0; i < ctx->tail_used; ++i)
+    if (ctx->tail[i].p) (void)hipFree(ctx->tail[i].p);
   if (ctx->arena) (void)hipFree(ctx->arena);
   delete ctx;
 }

@@ -241,7 +241,8 @@ template <int TYPE, typename OUT>
 __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
     OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate,
-    const float *__restrict__ res, int act, int tiles_m, int tiles_n) {
+    const float *__restrict__ res, int act, int tiles_m, int tiles_n, int full_tiles, int kparts,
+    float *__restrict__ partial) {
   using TT = bfrag::T<TYPE>;
   constexpr int kSteps = TT::kUnitK / kBK;
   // VALU instructions placed after each pair of MFMAs (the decode work per
@@ -249,11 +250,21 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   constexpr int kVpm = TYPE == Q8_0 ? 3 : (TYPE == Q4_K || TYPE == Q5_K) ? 6 : 8;
   __shared__ uint4 lds_a[4][kBM * kBK / 8];
 
-  const int total = tiles_m * tiles_n;
+  // Workgroups 0 .. full_tiles-1 run whole tiles (XCD-aware order over
+  // them); the rest run K part `part` of tail tile full_tiles + (w / kparts):
+  // the units [part * U / kparts, (part + 1) * U / kparts) of the U = k / 256,
+  // written raw to `partial` for gemm_tail_reduce_kernel.
   const int bid = blockIdx.x;
-  const int xcd = bid & 7, local = bid >> 3;
-  const int base = total >> 3, extra = total & 7;
-  const int v = xcd * base + (xcd < extra ? xcd : extra) + local;
+  int v, part = -1;
+  if (bid < full_tiles) {
+    const int xcd = bid & 7, local = bid >> 3;
+    const int base = full_tiles >> 3, extra = full_tiles & 7;
+    v = xcd * base + (xcd < extra ? xcd : extra) + local;
+  } else {
+    const int t = bid - full_tiles;
+    v = full_tiles + t / kparts;
+    part = t - (t / kparts) * kparts;
+  }
   const int mt = v / tiles_n, nt = v - mt * tiles_n;
 
   const int tid = threadIdx.x;
@@ -261,8 +272,11 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   const int l32 = lane & 31, h = lane >> 5;
   const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
   const int64_t m0 = (int64_t)mt * kBM;
-  const int64_t units = k / TT::kUnitK;
+  const int64_t all_units = k / TT::kUnitK;
+  const int64_t ub = part < 0 ? 0 : part * all_units / kparts;                  // first unit
+  const int64_t units = part < 0 ? all_units : (part + 1) * all_units / kparts - ub;
   const int64_t ksteps = units * kSteps;
+  a += ub * TT::kUnitK;  // A columns of this K range
   const int64_t wt_raw = (int64_t)nt * (kBN / kRowTile) + wave;
   const int64_t wt = wt_raw < ntiles_w ? wt_raw : ntiles_w - 1;  // keep reads in bounds
 
@@ -318,10 +332,10 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   // prologue: unit 0's weight bytes and scales, A(0) and A(1) into slots 0, 1;
   // step 0's slice-0 operands
 #pragma unroll
-  for (int j = 0; j < 2; ++j) TT::load_prep(raw[j], w, wt, l32 + 32 * j, 0, h);
+  for (int j = 0; j < 2; ++j) TT::load_prep(raw[j], w, wt, l32 + 32 * j, ub, h);
   static_for<kSteps>([&]<int G>() {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, 0, h);
+    for (int j = 0; j < 2; ++j) TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, ub, h);
   });
   dma_a(lds_a[0], 0);
   dma_a(lds_a[1], ksteps > 1 ? 1 : 0);
@@ -351,8 +365,8 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
             // slice is decoded.
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, un, h);
-              if constexpr (G == 0) TT::load_prep(raw[j], w, wt, l32 + 32 * j, un, h);
+              TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, ub + un, h);
+              if constexpr (G == 0) TT::load_prep(raw[j], w, wt, l32 + 32 * j, ub + un, h);
             }
             read_a(af[0], a_next, 0);
             if constexpr (G + 1 < kSteps) {
@@ -387,6 +401,17 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   // ---- epilogue: lane holds column l32 of each 32x32 tile, rows
   // 8*(e/4) + 4*h + (e%4).
   if (wt_raw >= ntiles_w) return;
+  if (part >= 0) {
+    // raw sums of this K part: tile-local row-major [256][256] f32 block
+    float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kBM * kBN) + 4 * h * kBN + wave * 64 + l32;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kBN + nb * 32] = acc[mb][nb][e];
+    return;
+  }
   const int64_t row0 = m0 + 4 * h;
   const int64_t col0 = wt_raw * kRowTile + l32;
   if (m0 + kBM <= m && wt_raw * kRowTile + kRowTile <= n && act == MQ_ACT_NONE_) {
@@ -473,24 +498,72 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   }
 }
 
+// Tail tiles split over K: y = epi(sum of the kparts raw sums in part order
+// + bias), one thread per 4 columns of a tile row.
+template <typename OUT>
+__global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__restrict__ partial, int kparts,
+                                                               int full_tiles, int tiles_n, int64_t m, int64_t n,
+                                                               OUT *__restrict__ y, int64_t ldy,
+                                                               const float *__restrict__ bias,
+                                                               const float *__restrict__ gate, int act) {
+  const int tl = blockIdx.y;                            // tail tile
+  const int idx = blockIdx.x * 256 + threadIdx.x;       // 0 .. 256 * 64 - 1
+  const int r = idx >> 6, c = (idx & 63) * 4;
+  const int v = full_tiles + tl;
+  const int mt = v / tiles_n, nt = v - mt * tiles_n;
+  const int64_t row = (int64_t)mt * kBM + r, col0 = (int64_t)nt * kBN + c;
+  if (row >= m) return;
+  const float *src = partial + (int64_t)tl * kparts * (kBM * kBN) + r * kBN + c;
+  float4 s = *reinterpret_cast<const float4 *>(src);
+  for (int p = 1; p < kparts; ++p) {
+    const float4 t = *reinterpret_cast<const float4 *>(src + (int64_t)p * (kBM * kBN));
+    s.x += t.x;
+    s.y += t.y;
+    s.z += t.z;
+    s.w += t.w;
+  }
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t col = col0 + j;
+    if (col < n) {
+      OUT *p = y + row * ldy + col;
+      store_epi<OUT>(p, reinterpret_cast<const float *>(p), apply_act(sv[j] + (bias ? bias[col] : 0.f), act), gate,
+                     gate ? gate[col] : 0.f);
+    }
+  }
+}
+
 template <int T>
 hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                             int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
-                            int act, hipStream_t stream) {
+                            int act, const GemmTail &tail, float *partial, hipStream_t stream) {
   const int tiles_m = (int)((m + kBM - 1) / kBM);
   const int tiles_n = (int)((n + kBN - 1) / kBN);
   const int grid = tiles_m * tiles_n;
-  // fast path: whole 256-wide units, 16-byte aligned rows, and element
-  // offsets of x that fit the kernel's 32-bit row offsets
-  const bool fast = (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
   const float *res = gate ? static_cast<const float *>(y) : nullptr;  // the gated update reads y, then writes it
-  if (fast) {
+  if (gemm_fast_ok(m, k, lda)) {
+    const bool split = partial && tail.kparts > 1;
+    const int full = split ? tail.full_tiles : grid;
+    const int kp = split ? tail.kparts : 1;
+    const int wgs = full + (grid - full) * kp;
     if (y_type == F32)
-      hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                         ntiles_w, a, m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n, k, ntiles_w, a,
+                         m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n, full, kp,
+                         partial);
     else
-      hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(grid), dim3(kFastThreads), 0, stream, w, n, k,
-                         ntiles_w, a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
+      hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n, k, ntiles_w,
+                         a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n, full, kp,
+                         partial);
+    if (split) {
+      const dim3 rgrid(kBM * kBN / 4 / 256, (unsigned)(grid - full));
+      if (y_type == F32)
+        hipLaunchKernelGGL(gemm_tail_reduce_kernel<float>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n, m,
+                           n, static_cast<float *>(y), ldy, bias, gate, act);
+      else
+        hipLaunchKernelGGL(gemm_tail_reduce_kernel<__bf16>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
+                           m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act);
+    }
   } else if (y_type == F32) {
     hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
                        a, m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
@@ -503,17 +576,38 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
 
 template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64_t, int64_t, const __bf16 *,
                                                    int64_t, int64_t, void *, int, int64_t, const float *,
-                                                   const float *, int, hipStream_t);
+                                                   const float *, int, const GemmTail &, float *, hipStream_t);
 
 #else  // the type dispatcher
 
+GemmTail gemm_tail_plan(int64_t m, int64_t n, int64_t k, int cus) {
+  const int64_t tiles = ((m + kGemmTile - 1) / kGemmTile) * ((n + kGemmTile - 1) / kGemmTile);
+  const int64_t rem = tiles % cus;                 // tiles of the last, partial round
+  const int64_t units = k / 256;
+  GemmTail t{(int)tiles, 1};
+  if (rem == 0 || units < 2) return t;
+  int64_t kp = cus / rem;                          // K parts per tail tile: they fill one round
+  kp = kp < units ? kp : units;
+  kp = kp < kGemmMaxKParts ? kp : kGemmMaxKParts;
+  if (kp < 2) return t;
+  t.full_tiles = (int)(tiles - rem);
+  t.kparts = (int)kp;
+  return t;
+}
+
+size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n) {
+  const int64_t tiles = ((m + kGemmTile - 1) / kGemmTile) * ((n + kGemmTile - 1) / kGemmTile);
+  if (t.kparts < 2) return 0;
+  return (size_t)(tiles - t.full_tiles) * t.kparts * kGemmTile * kGemmTile * sizeof(float);
+}
+
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,
                        int64_t m, int64_t lda, void *y, int y_type, int64_t ldy, const float *bias,
-                       const float *gate, int act, hipStream_t stream) {
+                       const float *gate, int act, const GemmTail &tail, float *partial, hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
   hipError_t err = hipErrorInvalidValue;
   dispatch_type(type, [&]<int T>() {
-    err = launch_gemm_type<T>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, stream);
+    err = launch_gemm_type<T>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
   });
   return err;
 }

@@ -37,14 +37,33 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const flo
 // multiple of 64 covering ceil(k/64)*64 zero-padded columns.  With `gate`
 // (f32 [n], f32 y only) the output is the gated residual update
 // y = y + gate * act(a . W^T + bias); without it y = act(a . W^T + bias).
+// Tiles are 256 x 256.  When the last round of tiles over the CUs is
+// partial, those tail tiles may split K into `kparts` workgroups that write
+// raw sums to `partial` (gemm_tail_bytes of it), added in part order by a
+// second kernel that applies the epilogue: the plan comes from
+// gemm_tail_plan; partial == NULL runs every tile whole.
+constexpr int kGemmTile = 256;
+constexpr int kGemmMaxKParts = 8;
+struct GemmTail {
+  int full_tiles;  // tiles run whole (all of them when kparts == 1)
+  int kparts;      // K parts per tail tile
+};
+GemmTail gemm_tail_plan(int64_t m, int64_t n, int64_t k, int cus);
+size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n);
+// The fast kernel (and tail splitting) applies: whole 256-wide K units,
+// 16-byte aligned rows and element offsets of x that fit 32 bits.
+inline bool gemm_fast_ok(int64_t m, int64_t k, int64_t lda) {
+  return (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
+}
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w,
                        const __bf16 *a, int64_t m, int64_t lda, void *y, int y_type, int64_t ldy,
-                       const float *bias, const float *gate, int act, hipStream_t stream);
+                       const float *bias, const float *gate, int act, const GemmTail &tail, float *partial,
+                       hipStream_t stream);
 // One weight type's launcher (instantiated in its own translation unit).
 template <int T>
 hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                             int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
-                            int act, hipStream_t stream);
+                            int act, const GemmTail &tail, float *partial, hipStream_t stream);
 
 // Epilogue activation (GELU with the tanh approximation, as candle's gelu()).
 __device__ __forceinline__ float apply_act(float v, int act) {

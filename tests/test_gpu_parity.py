@@ -463,6 +463,39 @@ def _sampled_rows_check(dev, torch, t, m, n, k, seed, rows=24):
     return err
 
 
+@pytest.mark.parametrize("m,tname,gated", [(2304, "Q4_K", False), (2300, "Q3_K", True)])
+def test_gemm_tail_tiles_split_k(dev, torch, m, tname, gated):
+    """270 tiles of 256 x 256 on 256 CUs: one full round plus 14 tail tiles, which the GEMM
+    splits over K into parts that a second kernel adds in order.  Every row of the tail
+    (the last 256-row panel, including a partial one) is checked against f64, as are
+    sampled rows of the full round; repeated calls are bit-identical."""
+    t = GgmlDType[tname]
+    n, k = 7680, 1024
+    _say(f"gemm tail split-K {tname} m={m} gated={gated}")
+    blocks = _weights(int(t), n, k, seed=m)
+    lin = mold_amd.Linear(QTensor.from_blocks(dev, t, (n, k), blocks),
+                          torch.from_numpy((np.random.default_rng(2).standard_normal(n) * 0.1).astype(np.float32)).cuda())
+    g = torch.Generator(device="cuda").manual_seed(m)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    if gated:
+        gate = torch.randn(n, device="cuda", generator=g)
+        res0 = torch.randn((m, n), device="cuda", generator=g)
+        outs = [lin.gated_add(x, gate, res0.clone()) for _ in range(2)]
+        y = outs[0] - res0
+    else:
+        outs = [lin.forward(x) for _ in range(2)]
+        y = outs[0]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    rows = np.concatenate([np.arange(2048, m), np.random.default_rng(m).choice(2048, size=16, replace=False)])
+    ref = O.matmul_f64(int(t), x[torch.from_numpy(rows).cuda()].cpu().numpy(), blocks, n, k) + lin.bias.cpu().numpy()
+    if gated:
+        ref = ref * gate.cpu().numpy()
+    got = y[torch.from_numpy(rows).cuda()].cpu().numpy()
+    assert np.isfinite(got).all()
+    assert O.rel_l2(got, ref) <= GEMM_TOL
+
+
 def test_full_flux_single_block_linear1_q4k(dev, torch):
     _say("full shape Q4_K 4608x3072->21504")
     _sampled_rows_check(dev, torch, GgmlDType.Q4_K, 4608, 21504, 3072, seed=4)
