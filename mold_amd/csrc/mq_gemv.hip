@@ -142,6 +142,32 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 constexpr int kQ4kMaxWaves = 16;
 constexpr size_t kQ4kMaxLds = 64 * 1024;
 
+// Cross-lane steps through DPP (no LDS round trip).  Lanes a step has no
+// source for (rows outside ROW_MASK) keep their own value.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
+}
+// Max over the wave, uniform: quad xor 1, quad xor 2, half-row mirror, row
+// mirror give every lane its 16-lane row's max; row_bcast:15 (rows 1, 3) and
+// row_bcast:31 (rows 2, 3) carry rows 0-2 into row 3; lane 63 holds the max.
+__device__ __forceinline__ float wave_max(float v) {
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0xB1, 0xF>(__float_as_int(v))));
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0x4E, 0xF>(__float_as_int(v))));
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0x141, 0xF>(__float_as_int(v))));
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0x140, 0xF>(__float_as_int(v))));
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0x142, 0xA>(__float_as_int(v))));
+  v = __builtin_fmaxf(v, __int_as_float(dpp<0x143, 0xC>(__float_as_int(v))));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// Sum over each aligned group of 8 lanes (a half row), in every lane of it.
+__device__ __forceinline__ int sum8(int v) {
+  v += dpp<0xB1, 0xF>(v);
+  v += dpp<0x4E, 0xF>(v);
+  v += dpp<0x141, 0xF>(v);
+  return v;
+}
+
 // LDS bytes of the Q4_K GEMV: Q8_K x (256 quants, d, 8 sub-block sums per
 // super-block and row of x) for all K, and the reduction.
 static size_t q4k_lds_bytes(int64_t nb, int m) {
@@ -205,9 +231,7 @@ __global__ __launch_bounds__(kQ4kMaxWaves * 64) void gemv_q4k_kernel(
       // occurrence in element order (lowest lane, lowest slot in the lane)
       const float a0 = __builtin_fabsf(xv[sb][m][0]), a1 = __builtin_fabsf(xv[sb][m][1]);
       const float a2 = __builtin_fabsf(xv[sb][m][2]), a3 = __builtin_fabsf(xv[sb][m][3]);
-      float amax = __builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3));
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+      const float amax = wave_max(__builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3)));
       const float cand = a0 == amax ? xv[sb][m][0]
                          : a1 == amax ? xv[sb][m][1]
                          : a2 == amax ? xv[sb][m][2]
@@ -229,9 +253,7 @@ __global__ __launch_bounds__(kQ4kMaxWaves * 64) void gemv_q4k_kernel(
         dx = 1.f / iscale;
       }
       xq[bg][m][lane] = packed;
-      qsum += __shfl_xor(qsum, 1);
-      qsum += __shfl_xor(qsum, 2);
-      qsum += __shfl_xor(qsum, 4);
+      qsum = sum8(qsum);
       if ((lane & 7) == 0) xb[bg][m][lane >> 3] = qsum;
       if (lane == 0) xd[bg][m] = dx;
     }
