@@ -514,24 +514,40 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
   const int64_t row = (int64_t)mt * kBM + r, col0 = (int64_t)nt * kBN + c;
   if (row >= m) return;
   const float *src = partial + (int64_t)tl * kparts * (kBM * kBN) + r * kBN + c;
-  float4 s = *reinterpret_cast<const float4 *>(src);
-  for (int p = 1; p < kparts; ++p) {
-    const float4 t = *reinterpret_cast<const float4 *>(src + (int64_t)p * (kBM * kBN));
-    s.x += t.x;
-    s.y += t.y;
-    s.z += t.z;
-    s.w += t.w;
-  }
-  const float sv[4] = {s.x, s.y, s.z, s.w};
+  // every part's load is issued before the first add (no chain of
+  // latencies), then the parts are added in order
+  float4 t[kGemmMaxKParts];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t col = col0 + j;
-    if (col < n) {
-      OUT *p = y + row * ldy + col;
-      store_epi<OUT>(p, reinterpret_cast<const float *>(p), apply_act(sv[j] + (bias ? bias[col] : 0.f), act), gate,
-                     gate ? gate[col] : 0.f);
+  for (int p = 0; p < kGemmMaxKParts; ++p)
+    if (p < kparts) t[p] = *reinterpret_cast<const float4 *>(src + (int64_t)p * (kBM * kBN));
+  float4 s = t[0];
+#pragma unroll
+  for (int p = 1; p < kGemmMaxKParts; ++p) {
+    if (p < kparts) {
+      s.x += t[p].x;
+      s.y += t[p].y;
+      s.z += t[p].z;
+      s.w += t[p].w;
     }
   }
+  const float sv[4] = {s.x, s.y, s.z, s.w};
+  OUT *yr = y + row * ldy + col0;
+  if constexpr (std::is_same_v<OUT, float>) {
+    if (gate) {
+      // the four residual values are read before any is written
+      float rv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rv[j] = col0 + j < n ? yr[j] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (col0 + j < n)
+          yr[j] = __builtin_fmaf(gate[col0 + j], apply_act(sv[j] + (bias ? bias[col0 + j] : 0.f), act), rv[j]);
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (col0 + j < n) store_out<OUT>(yr + j, apply_act(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
 }
 
 template <int T>
