@@ -463,15 +463,18 @@ def _sampled_rows_check(dev, torch, t, m, n, k, seed, rows=24):
     return err
 
 
-@pytest.mark.parametrize("m,tname,gated", [(2304, "Q4_K", False), (2300, "Q3_K", True)])
-def test_gemm_tail_tiles_split_k(dev, torch, m, tname, gated):
+@pytest.mark.parametrize("m,tname,mode", [(2304, "Q4_K", "plain"), (2300, "Q3_K", "gated"),
+                                          (2300, "Q2_K", "gelu_bf16")])
+def test_gemm_tail_tiles_split_k(dev, torch, m, tname, mode):
     """270 tiles of 256 x 256 on 256 CUs: one full round plus 14 tail tiles, which the GEMM
-    splits over K into parts that a second kernel adds in order.  Every row of the tail
+    splits over K into parts that a second kernel adds in order and passes through the
+    epilogue (plain f32, gated residual update, or GELU-tanh to bf16).  Every row of the tail
     (the last 256-row panel, including a partial one) is checked against f64, as are
     sampled rows of the full round; repeated calls are bit-identical."""
     t = GgmlDType[tname]
     n, k = 7680, 1024
-    _say(f"gemm tail split-K {tname} m={m} gated={gated}")
+    gated = mode == "gated"
+    _say(f"gemm tail split-K {tname} m={m} {mode}")
     blocks = _weights(int(t), n, k, seed=m)
     lin = mold_amd.Linear(QTensor.from_blocks(dev, t, (n, k), blocks),
                           torch.from_numpy((np.random.default_rng(2).standard_normal(n) * 0.1).astype(np.float32)).cuda())
@@ -482,15 +485,20 @@ def test_gemm_tail_tiles_split_k(dev, torch, m, tname, gated):
         res0 = torch.randn((m, n), device="cuda", generator=g)
         outs = [lin.gated_add(x, gate, res0.clone()) for _ in range(2)]
         y = outs[0] - res0
+    elif mode == "gelu_bf16":
+        outs = [lin.forward(x, act=mold_amd.ACT_GELU_TANH, out_dtype=torch.bfloat16) for _ in range(2)]
+        y = outs[0].float()
     else:
         outs = [lin.forward(x) for _ in range(2)]
         y = outs[0]
     torch.cuda.synchronize()
-    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     rows = np.concatenate([np.arange(2048, m), np.random.default_rng(m).choice(2048, size=16, replace=False)])
     ref = O.matmul_f64(int(t), x[torch.from_numpy(rows).cuda()].cpu().numpy(), blocks, n, k) + lin.bias.cpu().numpy()
     if gated:
         ref = ref * gate.cpu().numpy()
+    if mode == "gelu_bf16":
+        ref = 0.5 * ref * (1 + np.tanh(np.sqrt(2 / np.pi) * (ref + 0.044715 * ref ** 3)))
     got = y[torch.from_numpy(rows).cuda()].cpu().numpy()
     assert np.isfinite(got).all()
     assert O.rel_l2(got, ref) <= GEMM_TOL
