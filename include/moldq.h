@@ -134,6 +134,14 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
 int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, const float *shift,
                       const float *scale, float eps, void *out, int64_t ldo, void *stream);
 
+/* dst[r, :cols] = bf16(gelu_tanh(src[r, :cols])) (the tanh approximation,
+ * rounded once); src f32 16-byte aligned, dst bf16 8-byte aligned, cols and
+ * both row strides (elements) multiples of 4.  Replaces the single block's
+ * `mlp.gelu()` and the concatenation copy at
+ * crates/mold-inference/src/flux/offload.rs:390, 394. */
+int mq_gelu_tanh_bf16(const float *src, int64_t rows, int64_t cols, int64_t lds, void *dst, int64_t ldd,
+                      void *stream);
+
 /* For each of `rows` tokens and `heads` heads of the f32 projection output
  * qkv[r, 0:3*heads*128] (row stride ld; q, k, v blocks of heads*128): RmsNorm
  * of q and k (eps, bf16 weights [128]), RoPE rotating pair (2i, 2i+1) by the

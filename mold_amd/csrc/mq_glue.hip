@@ -1,4 +1,4 @@
-// mq_glue.hip — the two row-wise passes that sit between the quantized
+// mq_glue.hip — the row-wise passes that sit between the quantized
 // linears of a DiT block, each fused into one HBM pass:
 //
 //   * mq_adaln_modulate: LayerNorm without affine (eps) of each row, times
@@ -6,13 +6,16 @@
 //     attention / MLP linear (FLUX crates/mold-inference/src/flux/
 //     offload.rs:75-78 and :283-286, :374-377; Qwen-Image qwen_image/
 //     quantized_transformer.rs:913-922, :942-951).
+//   * mq_gelu_tanh_bf16: GELU-tanh of an f32 block into a bf16 block (FLUX
+//     single block's MLP half, offload.rs:390, 394, written straight into the
+//     concatenated linear2 input).
 //   * mq_qk_norm_rope: per token and head, RmsNorm (eps, bf16 weight) of q and
 //     k, RoPE on interleaved pairs, and the head split of q, k and v into bf16
 //     [heads, L, 128] at a row offset of a joint sequence: what the qkv
 //     projection output goes through before attention (FLUX offload.rs:
 //     188-201 and :56-66; Qwen-Image quantized_transformer.rs:739-751).
 //
-// Both are HBM-bound (f32 in, bf16 out, a few flops per byte).
+// All are HBM-bound (f32 in, bf16 out, a few flops per byte).
 #include "../../include/moldq.h"
 #include "mq_kernels.h"
 
@@ -122,6 +125,19 @@ __global__ __launch_bounds__(256) void adaln_modulate_kernel(const float *__rest
   }
 }
 
+// dst[r, c] = bf16(gelu_tanh(src[r, c])), four columns per thread (16-byte
+// loads, 8-byte stores), rows strided by gridDim.y.
+__global__ __launch_bounds__(256) void gelu_bf16_kernel(const float4 *__restrict__ src, int64_t rows, int64_t cols4,
+                                                        int64_t lds4, uint2 *__restrict__ dst, int64_t ldd4) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols4) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const float4 v = src[r * lds4 + c];
+    dst[r * ldd4 + c] = make_uint2(pack_bf16x2(apply_act(v.x, 1), apply_act(v.y, 1)),
+                                   pack_bf16x2(apply_act(v.z, 1), apply_act(v.w, 1)));
+  }
+}
+
 int invalid(const char *msg) { return set_error(MQ_E_INVALID, msg); }
 
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -162,6 +178,21 @@ int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, c
   if (rows == 0) return MQ_OK;
   hipLaunchKernelGGL(adaln_modulate_kernel, dim3((unsigned)rows), dim3(256), 0, static_cast<hipStream_t>(stream), x,
                      ldx, cols, shift, scale, eps, static_cast<uint2 *>(out), ldo);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
+}
+
+int mq_gelu_tanh_bf16(const float *src, int64_t rows, int64_t cols, int64_t lds, void *dst, int64_t ldd,
+                      void *stream) {
+  if (rows < 0 || cols <= 0 || cols % 4 || lds < cols || ldd < cols || lds % 4 || ldd % 4)
+    return invalid("mq_gelu_tanh_bf16: cols and row strides must be multiples of 4 with strides >= cols");
+  if (!src || !dst) return invalid("mq_gelu_tanh_bf16: NULL pointer");
+  if (!aligned(src, 16) || !aligned(dst, 8)) return invalid("mq_gelu_tanh_bf16: misaligned buffer");
+  if (rows == 0) return MQ_OK;
+  const int64_t cols4 = cols / 4;
+  const dim3 grid((unsigned)((cols4 + 255) / 256), (unsigned)(rows < 65535 ? rows : 65535));
+  hipLaunchKernelGGL(gelu_bf16_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const float4 *>(src), rows, cols4, lds / 4, static_cast<uint2 *>(dst), ldd / 4);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
 }

@@ -423,7 +423,11 @@ class FluxStep:
             a = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
         cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
         cat[:, :h] = a
-        cat[:, h:] = gelu_tanh(y[:, 3 * h:])
+        if self._fused(x):
+            from .fused import gelu_tanh_bf16
+            gelu_tanh_bf16(y[:, 3 * h:], cat[:, h:])
+        else:
+            cat[:, h:] = gelu_tanh(y[:, 3 * h:])
         return self._gated(p + "linear2", cat, gate, x)
 
     def stems(self, img, txt, t, guidance, y):

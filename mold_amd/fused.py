@@ -1,7 +1,7 @@
 """Fused block glue on the device: libmoldq's row passes between the quantized
-linears (mq_adaln_modulate, mq_qk_norm_rope in include/moldq.h).
+linears (mq_adaln_modulate, mq_gelu_tanh_bf16, mq_qk_norm_rope in include/moldq.h).
 
-Both run on torch's current stream and allocate only their outputs.  They need
+All run on torch's current stream and allocate only their outputs.  They need
 the HIP library (no fallback); the host-CPU path of the block graphs keeps the
 equivalent torch ops.
 """
@@ -30,6 +30,19 @@ def adaln_modulate(x, shift, scale, eps: float = 1e-6, out=None):
         out = torch.empty((rows, cols), dtype=torch.bfloat16, device=x.device)
     check(_lib.load().mq_adaln_modulate(x.data_ptr(), rows, cols, x.stride(0), shift.data_ptr(), scale.data_ptr(),
                                         float(eps), out.data_ptr(), out.stride(0), _stream_ptr()))
+    return out
+
+
+def gelu_tanh_bf16(src, out):
+    """out[:] = bf16(gelu_tanh(src)) for src f32 [rows, cols] and out bf16 [rows, cols],
+    both with unit column stride (row strides free, multiples of 4)."""
+    import torch
+    if src.dtype != torch.float32 or out.dtype != torch.bfloat16 or src.dim() != 2 or tuple(out.shape) != tuple(src.shape) \
+            or src.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("gelu_tanh_bf16: src f32 and out bf16 of one 2-D shape with unit column stride")
+    rows, cols = src.shape
+    check(_lib.load().mq_gelu_tanh_bf16(src.data_ptr(), rows, cols, src.stride(0), out.data_ptr(), out.stride(0),
+                                        _stream_ptr()))
     return out
 
 

@@ -80,6 +80,26 @@ def test_qk_norm_rope_matches_reference(rows, heads, extra, row_off, l_total):
     assert bool((q[:, :row_off] == 7.0).all()) and bool((q[:, row_off + rows:] == 7.0).all())
 
 
+@pytest.mark.parametrize("rows,cols,lds,ldd,off", [(37, 12288, 21504, 15360, 9216), (5, 8, 8, 12, 0)])
+def test_gelu_tanh_bf16_matches_reference(rows, cols, lds, ldd, off):
+    """GELU-tanh of a strided f32 block into a strided bf16 block (the FLUX single block's
+    MLP half written into linear2's concatenated input): within one bf16 ulp of f64, and
+    the destination's other columns untouched."""
+    print(f"[case] gelu_bf16 rows={rows} cols={cols}", flush=True)
+    mold_amd.load()
+    g = torch.Generator().manual_seed(rows + cols)
+    src = (torch.randn((rows, lds), generator=g) * 3).cuda()
+    dst = torch.full((rows, ldd), 5.0, dtype=torch.bfloat16, device="cuda")
+    sv = src[:, off:off + cols]
+    dv = dst[:, ldd - cols:]
+    FU.gelu_tanh_bf16(sv, dv)
+    torch.cuda.synchronize()
+    xd = sv.double().cpu()
+    ref = 0.5 * xd * (1 + torch.tanh(np.sqrt(2 / np.pi) * (xd + 0.044715 * xd ** 3)))
+    assert _within_one_ulp(dv, ref)
+    assert bool((dst[:, :ldd - cols] == 5.0).all())
+
+
 def test_glue_errors_are_reported():
     mold_amd.load()
     y = torch.zeros((4, 3 * 128), device="cuda")
