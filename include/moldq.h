@@ -134,25 +134,27 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
 int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, const float *shift,
                       const float *scale, float eps, void *out, int64_t ldo, void *stream);
 
-/* dst[r, :cols] = bf16(gelu_tanh(src[r, :cols])) (the tanh approximation,
- * rounded once); src f32 16-byte aligned, dst bf16 8-byte aligned, cols and
- * both row strides (elements) multiples of 4.  Replaces the single block's
- * `mlp.gelu()` and the concatenation copy at
+/* dst[r, :cols] = bf16(gelu_tanh(src[r, :cols])) (the tanh approximation in
+ * f32, rounded once); src F32 (16-byte aligned) or BF16 (8-byte aligned), dst
+ * bf16 8-byte aligned, cols and both row strides (elements) multiples of 4.
+ * Replaces the single block's `mlp.gelu()` and the concatenation copy at
  * crates/mold-inference/src/flux/offload.rs:390, 394. */
-int mq_gelu_tanh_bf16(const float *src, int64_t rows, int64_t cols, int64_t lds, void *dst, int64_t ldd,
-                      void *stream);
+int mq_gelu_tanh_bf16(const void *src, int src_dtype, int64_t rows, int64_t cols, int64_t lds, void *dst,
+                      int64_t ldd, void *stream);
 
-/* For each of `rows` tokens and `heads` heads of the f32 projection output
- * qkv[r, 0:3*heads*128] (row stride ld; q, k, v blocks of heads*128): RmsNorm
+/* For each of `rows` tokens and `heads` heads of the projection output
+ * qkv[r, 0:3*heads*128] (qkv_dtype F32 or BF16, row stride ld; q, k, v blocks
+ * of heads*128), computed in f32: RmsNorm
  * of q and k (eps, bf16 weights [128]), RoPE rotating pair (2i, 2i+1) by the
  * angle whose cos / sin are cos_table / sin_table[r, i] (f32 [rows, 64]), and
  * q, k, v written as bf16 [heads, l_total, 128] at rows row_off .. row_off +
  * rows - 1.  head_dim must be 128.  Replaces QkNorm + apply_rope + the head
  * split at crates/mold-inference/src/flux/offload.rs:188-201, 56-66 and
  * crates/mold-inference/src/qwen_image/quantized_transformer.rs:739-757. */
-int mq_qk_norm_rope(const float *qkv, int64_t ld, int64_t rows, int heads, int head_dim, const void *q_weight,
-                    const void *k_weight, float eps, const float *cos_table, const float *sin_table, void *q_out,
-                    void *k_out, void *v_out, int64_t row_off, int64_t l_total, void *stream);
+int mq_qk_norm_rope(const void *qkv, int qkv_dtype, int64_t ld, int64_t rows, int heads, int head_dim,
+                    const void *q_weight, const void *k_weight, float eps, const float *cos_table,
+                    const float *sin_table, void *q_out, void *k_out, void *v_out, int64_t row_off, int64_t l_total,
+                    void *stream);
 
 /* The DiT blocks' gated residual update through one quantized linear:
  * y[m, :n] += gate[:n] * (x[m, :k] . W^T + bias), y f32 (row stride ldy),

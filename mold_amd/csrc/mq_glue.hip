@@ -15,7 +15,7 @@
 //     projection output goes through before attention (FLUX offload.rs:
 //     188-201 and :56-66; Qwen-Image quantized_transformer.rs:739-751).
 //
-// All are HBM-bound (f32 in, bf16 out, a few flops per byte).
+// All are HBM-bound (f32 or bf16 in, bf16 out, a few flops per byte).
 #include "../../include/moldq.h"
 #include "mq_kernels.h"
 
@@ -45,8 +45,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 
 // One wave per (token, head); lane i owns the pair (2i, 2i+1), which is also
 // RoPE's rotation pair i.  Four waves per workgroup.
+__device__ __forceinline__ float2 load2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
+__device__ __forceinline__ float2 load2(const __bf16 *p) {
+  uint32_t u = *reinterpret_cast<const uint32_t *>(p);
+  return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xFFFF0000u));
+}
+__device__ __forceinline__ float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ float4 load4(const __bf16 *p) {
+  const uint2 u = *reinterpret_cast<const uint2 *>(p);
+  return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                     __uint_as_float(u.y & 0xFFFF0000u));
+}
+
+template <typename IN>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
-    const float *__restrict__ qkv, int64_t ld, int64_t rows, int heads, const __bf16 *__restrict__ qw,
+    const IN *__restrict__ qkv, int64_t ld, int64_t rows, int heads, const __bf16 *__restrict__ qw,
     const __bf16 *__restrict__ kw, float eps, const float *__restrict__ cosv, const float *__restrict__ sinv,
     uint32_t *__restrict__ qo, uint32_t *__restrict__ ko, uint32_t *__restrict__ vo, int64_t row_off,
     int64_t l_total) {
@@ -55,10 +68,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   if (item >= rows * heads) return;  // whole waves
   const int64_t l = item / heads;
   const int h = (int)(item - l * heads);
-  const float *src = qkv + l * ld + (int64_t)h * kHead + 2 * lane;
-  const float2 q = *reinterpret_cast<const float2 *>(src);
-  const float2 k = *reinterpret_cast<const float2 *>(src + (int64_t)heads * kHead);
-  const float2 v = *reinterpret_cast<const float2 *>(src + 2 * (int64_t)heads * kHead);
+  const IN *src = qkv + l * ld + (int64_t)h * kHead + 2 * lane;
+  const float2 q = load2(src);
+  const float2 k = load2(src + (int64_t)heads * kHead);
+  const float2 v = load2(src + 2 * (int64_t)heads * kHead);
   const float c = cosv[l * (kHead / 2) + lane], s = sinv[l * (kHead / 2) + lane];
   const float rq = rsqrtf(wave_sum(q.x * q.x + q.y * q.y) / kHead + eps);
   const float rk = rsqrtf(wave_sum(k.x * k.x + k.y * k.y) / kHead + eps);
@@ -127,12 +140,13 @@ __global__ __launch_bounds__(256) void adaln_modulate_kernel(const float *__rest
 
 // dst[r, c] = bf16(gelu_tanh(src[r, c])), four columns per thread (16-byte
 // loads, 8-byte stores), rows strided by gridDim.y.
-__global__ __launch_bounds__(256) void gelu_bf16_kernel(const float4 *__restrict__ src, int64_t rows, int64_t cols4,
-                                                        int64_t lds4, uint2 *__restrict__ dst, int64_t ldd4) {
+template <typename IN>
+__global__ __launch_bounds__(256) void gelu_bf16_kernel(const IN *__restrict__ src, int64_t rows, int64_t cols4,
+                                                        int64_t lds, uint2 *__restrict__ dst, int64_t ldd4) {
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (c >= cols4) return;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
-    const float4 v = src[r * lds4 + c];
+    const float4 v = load4(src + r * lds + 4 * c);
     dst[r * ldd4 + c] = make_uint2(pack_bf16x2(apply_act(v.x, 1), apply_act(v.y, 1)),
                                    pack_bf16x2(apply_act(v.z, 1), apply_act(v.w, 1)));
   }
@@ -146,23 +160,32 @@ bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 extern "C" {
 
-int mq_qk_norm_rope(const float *qkv, int64_t ld, int64_t rows, int heads, int head_dim, const void *q_weight,
-                    const void *k_weight, float eps, const float *cos_table, const float *sin_table, void *q_out,
-                    void *k_out, void *v_out, int64_t row_off, int64_t l_total, void *stream) {
+int mq_qk_norm_rope(const void *qkv, int qkv_dtype, int64_t ld, int64_t rows, int heads, int head_dim,
+                    const void *q_weight, const void *k_weight, float eps, const float *cos_table,
+                    const float *sin_table, void *q_out, void *k_out, void *v_out, int64_t row_off, int64_t l_total,
+                    void *stream) {
   if (head_dim != kHead) return invalid("mq_qk_norm_rope: head_dim must be 128");
+  if (qkv_dtype != MQ_F32 && qkv_dtype != MQ_BF16) return invalid("mq_qk_norm_rope: qkv dtype must be F32 or BF16");
   if (rows < 0 || heads <= 0 || row_off < 0 || row_off + rows > l_total)
     return invalid("mq_qk_norm_rope: rows, heads or row range out of bounds");
   if (ld < 3 * (int64_t)heads * kHead || ld % 2) return invalid("mq_qk_norm_rope: ld must be even and >= 3*heads*128");
   if (!qkv || !q_weight || !k_weight || !cos_table || !sin_table || !q_out || !k_out || !v_out)
     return invalid("mq_qk_norm_rope: NULL pointer");
-  if (!aligned(qkv, 8) || !aligned(q_out, 4) || !aligned(k_out, 4) || !aligned(v_out, 4))
+  if (!aligned(qkv, qkv_dtype == MQ_F32 ? 8 : 4) || !aligned(q_out, 4) || !aligned(k_out, 4) || !aligned(v_out, 4))
     return invalid("mq_qk_norm_rope: misaligned buffer");
   if (rows == 0) return MQ_OK;
   const int64_t items = rows * heads;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), qkv, ld, rows, heads, static_cast<const __bf16 *>(q_weight),
-                     static_cast<const __bf16 *>(k_weight), eps, cos_table, sin_table, static_cast<uint32_t *>(q_out),
-                     static_cast<uint32_t *>(k_out), static_cast<uint32_t *>(v_out), row_off, l_total);
+  const dim3 grid((unsigned)((items + 3) / 4));
+  const __bf16 *qw = static_cast<const __bf16 *>(q_weight), *kw = static_cast<const __bf16 *>(k_weight);
+  uint32_t *qo = static_cast<uint32_t *>(q_out), *ko = static_cast<uint32_t *>(k_out), *vo = static_cast<uint32_t *>(v_out);
+  if (qkv_dtype == MQ_F32)
+    hipLaunchKernelGGL(qk_norm_rope_kernel<float>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const float *>(qkv), ld, rows, heads, qw, kw, eps, cos_table, sin_table, qo, ko, vo,
+                       row_off, l_total);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_kernel<__bf16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const __bf16 *>(qkv), ld, rows, heads, qw, kw, eps, cos_table, sin_table, qo, ko,
+                       vo, row_off, l_total);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
 }
@@ -182,17 +205,23 @@ int mq_adaln_modulate(const float *x, int64_t rows, int64_t cols, int64_t ldx, c
   return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
 }
 
-int mq_gelu_tanh_bf16(const float *src, int64_t rows, int64_t cols, int64_t lds, void *dst, int64_t ldd,
-                      void *stream) {
+int mq_gelu_tanh_bf16(const void *src, int src_dtype, int64_t rows, int64_t cols, int64_t lds, void *dst,
+                      int64_t ldd, void *stream) {
+  if (src_dtype != MQ_F32 && src_dtype != MQ_BF16) return invalid("mq_gelu_tanh_bf16: src dtype must be F32 or BF16");
   if (rows < 0 || cols <= 0 || cols % 4 || lds < cols || ldd < cols || lds % 4 || ldd % 4)
     return invalid("mq_gelu_tanh_bf16: cols and row strides must be multiples of 4 with strides >= cols");
   if (!src || !dst) return invalid("mq_gelu_tanh_bf16: NULL pointer");
-  if (!aligned(src, 16) || !aligned(dst, 8)) return invalid("mq_gelu_tanh_bf16: misaligned buffer");
+  if (!aligned(src, src_dtype == MQ_F32 ? 16 : 8) || !aligned(dst, 8))
+    return invalid("mq_gelu_tanh_bf16: misaligned buffer");
   if (rows == 0) return MQ_OK;
   const int64_t cols4 = cols / 4;
   const dim3 grid((unsigned)((cols4 + 255) / 256), (unsigned)(rows < 65535 ? rows : 65535));
-  hipLaunchKernelGGL(gelu_bf16_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
-                     reinterpret_cast<const float4 *>(src), rows, cols4, lds / 4, static_cast<uint2 *>(dst), ldd / 4);
+  if (src_dtype == MQ_F32)
+    hipLaunchKernelGGL(gelu_bf16_kernel<float>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const float *>(src), rows, cols4, lds, static_cast<uint2 *>(dst), ldd / 4);
+  else
+    hipLaunchKernelGGL(gelu_bf16_kernel<__bf16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const __bf16 *>(src), rows, cols4, lds, static_cast<uint2 *>(dst), ldd / 4);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
 }

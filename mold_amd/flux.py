@@ -286,6 +286,8 @@ class FluxStep:
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
         self.fused = fused
         self.gated_epilogue = True
+        # fused path: projections that feed only the fused passes (qkv, linear1) are written in bf16
+        self.bf16_projections = True
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused) for the modulate and the
@@ -374,19 +376,19 @@ class FluxStep:
         library context's shared staging scratch."""
         import torch
         from .fused import new_heads, qk_norm_rope
-        f32 = torch.float32
+        bf16 = torch.bfloat16 if self.bf16_projections else torch.float32  # qkv feeds only the fused pass
         lt, H = txt.shape[0], self.cfg.num_heads
         q, k, v = new_heads(H, lt + img.shape[0], img.device)
         main = torch.cuda.current_stream(img.device)
         aux = aux_stream(img.device)
         aux.wait_stream(main)
         with torch.cuda.stream(aux):
-            ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, tm[0], tm[1]), out_dtype=f32)
+            ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, tm[0], tm[1]), out_dtype=bf16)
             qk_norm_rope(ty, H, self.p.dense[p + "txt_attn.norm.query_norm.scale"],
                          self.p.dense[p + "txt_attn.norm.key_norm.scale"], cos[:lt], sin[:lt], q, k, v, 0)
         for t in (txt, tm[0], q, k, v, cos, sin):
             t.record_stream(aux)
-        iy = self.p.lin[p + "img_attn.qkv"].forward(self._modulate(img, im[0], im[1]), out_dtype=f32)
+        iy = self.p.lin[p + "img_attn.qkv"].forward(self._modulate(img, im[0], im[1]), out_dtype=bf16)
         qk_norm_rope(iy, H, self.p.dense[p + "img_attn.norm.query_norm.scale"],
                      self.p.dense[p + "img_attn.norm.key_norm.scale"], cos[lt:], sin[lt:], q, k, v, lt)
         main.wait_stream(aux)
@@ -411,7 +413,9 @@ class FluxStep:
         cfg = self.cfg
         p = f"single_blocks.{i}."
         shift, scale, gate = self._mod(p + "modulation.lin", vec, 3)
-        y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
+        # on the fused path linear1's output feeds only the norm/RoPE and GELU passes: bf16
+        y_dtype = torch.bfloat16 if self._fused(x) and self.bf16_projections else torch.float32
+        y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=y_dtype)
         L, h = x.shape[0], cfg.hidden_size
         if self._fused(x):
             a = self.attn(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")], cos, sin))

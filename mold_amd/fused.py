@@ -34,15 +34,16 @@ def adaln_modulate(x, shift, scale, eps: float = 1e-6, out=None):
 
 
 def gelu_tanh_bf16(src, out):
-    """out[:] = bf16(gelu_tanh(src)) for src f32 [rows, cols] and out bf16 [rows, cols],
+    """out[:] = bf16(gelu_tanh(src)) for src f32 or bf16 [rows, cols] and out bf16 [rows, cols],
     both with unit column stride (row strides free, multiples of 4)."""
     import torch
-    if src.dtype != torch.float32 or out.dtype != torch.bfloat16 or src.dim() != 2 or tuple(out.shape) != tuple(src.shape) \
-            or src.stride(1) != 1 or out.stride(1) != 1:
-        raise ValueError("gelu_tanh_bf16: src f32 and out bf16 of one 2-D shape with unit column stride")
+    from .quantized import _dtype_code
+    if src.dtype not in (torch.float32, torch.bfloat16) or out.dtype != torch.bfloat16 or src.dim() != 2 \
+            or tuple(out.shape) != tuple(src.shape) or src.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("gelu_tanh_bf16: src f32/bf16 and out bf16 of one 2-D shape with unit column stride")
     rows, cols = src.shape
-    check(_lib.load().mq_gelu_tanh_bf16(src.data_ptr(), rows, cols, src.stride(0), out.data_ptr(), out.stride(0),
-                                        _stream_ptr()))
+    check(_lib.load().mq_gelu_tanh_bf16(src.data_ptr(), _dtype_code(src.dtype), rows, cols, src.stride(0),
+                                        out.data_ptr(), out.stride(0), _stream_ptr()))
     return out
 
 
@@ -55,12 +56,13 @@ def new_heads(heads: int, l_total: int, device):
 def qk_norm_rope(qkv, heads: int, q_weight, k_weight, cos, sin, q_out, k_out, v_out, row_off: int,
                  eps: float = 1e-6):
     """RmsNorm(q), RmsNorm(k), RoPE and the head split of one segment's projection
-    output qkv f32 [rows, >= 3*heads*128] (q | k | v column blocks) into bf16
+    output qkv f32 or bf16 [rows, >= 3*heads*128] (q | k | v column blocks) into bf16
     [heads, l_total, 128] at rows row_off ..; cos / sin f32 [rows, 64] for the
     segment's tokens; q_weight / k_weight bf16 [128]."""
     import torch
-    if qkv.dtype != torch.float32 or qkv.dim() != 2 or qkv.stride(1) != 1:
-        raise ValueError("qk_norm_rope: qkv must be a 2-D f32 tensor with unit column stride")
+    from .quantized import _dtype_code
+    if qkv.dtype not in (torch.float32, torch.bfloat16) or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qk_norm_rope: qkv must be a 2-D f32 or bf16 tensor with unit column stride")
     rows = qkv.shape[0]
     for t in (cos, sin):
         if t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (rows, HEAD_DIM // 2):
@@ -72,7 +74,8 @@ def qk_norm_rope(qkv, heads: int, q_weight, k_weight, cos, sin, q_out, k_out, v_
     for t in (q_out, k_out, v_out):
         if t.dtype != torch.bfloat16 or not t.is_contiguous() or tuple(t.shape) != (heads, l_total, HEAD_DIM):
             raise ValueError("qk_norm_rope: outputs must be contiguous bf16 [heads, l_total, 128]")
-    check(_lib.load().mq_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), rows, heads, HEAD_DIM, q_weight.data_ptr(),
+    check(_lib.load().mq_qk_norm_rope(qkv.data_ptr(), _dtype_code(qkv.dtype), qkv.stride(0), rows, heads, HEAD_DIM,
+                                      q_weight.data_ptr(),
                                       k_weight.data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(),
                                       q_out.data_ptr(), k_out.data_ptr(), v_out.data_ptr(), row_off, l_total,
                                       _stream_ptr()))

@@ -230,6 +230,8 @@ class QwenImageStep:
         self.gemm_dtype = torch.bfloat16 if gemm_dtype is None else gemm_dtype
         self.overlap = overlap
         self.gated_epilogue = True
+        # fused path: the qkv projections, which feed only the fused pass, are written in bf16
+        self.bf16_projections = True
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused): on the GPU with bf16 GEMM inputs."""
@@ -256,7 +258,8 @@ class QwenImageStep:
         bf16 buffers `heads` = (q, k, v) at rows 0 .. L_txt - 1 (fused path)."""
         t_s1, t_c1 = mods[0], mods[1]
         import torch
-        y = self.p.lin[p + "attn.add_qkv_proj"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=torch.float32)
+        y_dtype = torch.bfloat16 if heads is not None and self.bf16_projections else torch.float32
+        y = self.p.lin[p + "attn.add_qkv_proj"].forward(self._modulate(txt, t_s1, t_c1), out_dtype=y_dtype)
         if heads is not None:
             from .fused import qk_norm_rope
             qk_norm_rope(y, self.cfg.num_attention_heads, self.p.dense[p + "attn.norm_added_q.weight"],
@@ -309,7 +312,9 @@ class QwenImageStep:
                 t.record_stream(aux)
             for t in (tqkv if tqkv is not None else ()):
                 t.record_stream(main)
-        y = self.p.lin[p + "attn.to_qkv"].forward(self._modulate(img, i_mod[0], i_mod[1]), out_dtype=torch.float32)
+        y = self.p.lin[p + "attn.to_qkv"].forward(self._modulate(img, i_mod[0], i_mod[1]),
+                                                 out_dtype=torch.bfloat16 if fused and self.bf16_projections
+                                                 else torch.float32)
         if fused:
             from .fused import qk_norm_rope
             qk_norm_rope(y, self.cfg.num_attention_heads, self.p.dense[p + "attn.norm_q.weight"],

@@ -45,15 +45,18 @@ def test_adaln_modulate_matches_reference(rows, cols, ld):
     assert _within_one_ulp(out, ref)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("rows,heads,extra,row_off,l_total", [(37, 3, 64, 5, 50), (512, 24, 0, 0, 512),
                                                               (64, 2, 12288 - 768, 100, 164)])
-def test_qk_norm_rope_matches_reference(rows, heads, extra, row_off, l_total):
-    print(f"[case] qk_norm_rope rows={rows} heads={heads} off={row_off}", flush=True)
+def test_qk_norm_rope_matches_reference(rows, heads, extra, row_off, l_total, dtype):
+    print(f"[case] qk_norm_rope rows={rows} heads={heads} off={row_off} {dtype}", flush=True)
     mold_amd.load()
     g = torch.Generator().manual_seed(rows * heads)
     d = 128
     ld = 3 * heads * d + extra
     y = (torch.randn((rows, ld), generator=g) * 2).cuda()
+    if dtype == "bf16":
+        y = y.to(torch.bfloat16)
     qw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
     kw = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).cuda()
     ang = torch.rand((rows, d // 2), generator=g, dtype=torch.float64) * 50
@@ -74,14 +77,15 @@ def test_qk_norm_rope_matches_reference(rows, heads, extra, row_off, l_total):
     sl = slice(row_off, row_off + rows)
     assert _within_one_ulp(q[:, sl], norm_rope(yd[0], qw))
     assert _within_one_ulp(k[:, sl], norm_rope(yd[1], kw))
-    vref = y[:, 2 * heads * d:3 * heads * d].reshape(rows, heads, d).transpose(0, 1).to(torch.bfloat16)
+    vref = y[:, 2 * heads * d:3 * heads * d].reshape(rows, heads, d).transpose(0, 1).float().to(torch.bfloat16)
     assert torch.equal(v[:, sl].view(torch.int16), vref.view(torch.int16))
     # rows outside the segment are untouched
     assert bool((q[:, :row_off] == 7.0).all()) and bool((q[:, row_off + rows:] == 7.0).all())
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("rows,cols,lds,ldd,off", [(37, 12288, 21504, 15360, 9216), (5, 8, 8, 12, 0)])
-def test_gelu_tanh_bf16_matches_reference(rows, cols, lds, ldd, off):
+def test_gelu_tanh_bf16_matches_reference(rows, cols, lds, ldd, off, dtype):
     """GELU-tanh of a strided f32 block into a strided bf16 block (the FLUX single block's
     MLP half written into linear2's concatenated input): within one bf16 ulp of f64, and
     the destination's other columns untouched."""
@@ -89,6 +93,8 @@ def test_gelu_tanh_bf16_matches_reference(rows, cols, lds, ldd, off):
     mold_amd.load()
     g = torch.Generator().manual_seed(rows + cols)
     src = (torch.randn((rows, lds), generator=g) * 3).cuda()
+    if dtype == "bf16":
+        src = src.to(torch.bfloat16)
     dst = torch.full((rows, ldd), 5.0, dtype=torch.bfloat16, device="cuda")
     sv = src[:, off:off + cols]
     dv = dst[:, ldd - cols:]
@@ -107,8 +113,8 @@ def test_glue_errors_are_reported():
     w = torch.ones(128, dtype=torch.bfloat16, device="cuda")
     q, k, v = FU.new_heads(1, 4, "cuda")
     lib = mold_amd.load()
-    rc = lib.mq_qk_norm_rope(y.data_ptr(), y.stride(0), 4, 1, 64, w.data_ptr(), w.data_ptr(), 1e-6, cs.data_ptr(),
-                             cs.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, 4, None)
+    rc = lib.mq_qk_norm_rope(y.data_ptr(), 0, y.stride(0), 4, 1, 64, w.data_ptr(), w.data_ptr(), 1e-6,
+                             cs.data_ptr(), cs.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), 0, 4, None)
     assert rc == -1 and b"head_dim" in lib.mq_last_error()
     with pytest.raises(MoldqError):   # row range past the joint sequence
         FU.qk_norm_rope(y, 1, w, w, cs, cs, q, k, v, 2)
