@@ -229,27 +229,49 @@ def aux_stream(device):
 ATTENTION_BACKEND = {"name": None}
 
 
-def attention_bf16(q, k, v):
-    """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] f32 -> [L, H*D] bf16.
+ATTN_ROWS = 256  # the fused paths pad the joint sequence to a multiple of this
 
-    Runs PyTorch's fused flash / memory-efficient attention in bf16 (f32 softmax
-    accumulation inside).  Where neither fused kernel exists for the device, it
-    falls back to head-chunked bf16 products with f32 softmax; the right operand
-    of every batched product is made contiguous first (k^T explicitly), the form
-    that is safe for bf16 batched GEMMs on this platform.  The backend used is
-    recorded in ATTENTION_BACKEND."""
+
+def padded_len(n: int) -> int:
+    return (n + ATTN_ROWS - 1) // ATTN_ROWS * ATTN_ROWS
+
+
+def attention_bf16(q, k, v, valid: Optional[int] = None):
+    """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] -> [valid, H*D] bf16.
+
+    Runs PyTorch's fused attention in bf16 (f32 softmax accumulation inside).
+    `valid` < L marks rows valid .. L-1 as padding whose k and v rows are zero:
+    the fused kernels run much faster at lengths that are multiples of 256
+    (1.0 vs 2.0 ms at 24 x 7168 vs 7145 tokens on an MI355X), and zero keys are
+    removed exactly afterwards.  Each of the n_pad zero keys adds exp(0) = 1 to
+    a row's softmax denominator Z and nothing to its numerator, so with the
+    log-sum-exp the kernel returns, out = out_pad / (1 - n_pad exp(-lse)).
+    Where neither fused kernel exists for the device, it falls back to
+    head-chunked bf16 products with f32 softmax on the valid rows; the right
+    operand of every batched product is made contiguous first (k^T explicitly),
+    the form that is safe for bf16 batched GEMMs on this platform.  The backend
+    used is recorded in ATTENTION_BACKEND."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
     h, l, d = q.shape
+    valid = l if valid is None else valid
     qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
     if ATTENTION_BACKEND["name"] in (None, "fused"):
         try:
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
+            if valid < l:
+                out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
+                                                                                  True)[:2]
+                fac = 1.0 / (1.0 - (l - valid) * torch.exp(-lse[0, :, :valid]))
+                o = (out[0, :, :valid].float() * fac[..., None]).to(torch.bfloat16)
+            else:
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
             ATTENTION_BACKEND["name"] = "fused"
-            return o.transpose(0, 1).reshape(l, h * d)
+            return o.transpose(0, 1).reshape(valid, h * d)
         except RuntimeError:
             ATTENTION_BACKEND["name"] = "chunked"
+    qb, kb, vb = qb[:, :valid], kb[:, :valid], vb[:, :valid]
+    l = valid
     out = torch.empty((l, h * d), dtype=torch.bfloat16, device=q.device)
     scale = 1.0 / math.sqrt(d)
     step = max(1, min(h, (1 << 31) // max(1, l * l * 4)))
@@ -325,12 +347,18 @@ class FluxStep:
             return self.p.lin[name].gated_add(h, gate, res)
         return res + gate * self.p.lin[name].forward(h, out_dtype=torch.float32)
 
+    def _attn_padded(self, q, k, v, valid):
+        """Attention over the fused path's padded joint buffers (rows >= valid zero)."""
+        if self.attn is attention_bf16:
+            return attention_bf16(q, k, v, valid)
+        return self.attn(q[:, :valid], k[:, :valid], v[:, :valid])
+
     def _heads_fused(self, segments, cos, sin):
         """q, k, v bf16 [H, L, D] of the joint sequence from (qkv f32 [L_seg, >= 3h],
         query-norm name, key-norm name) segments in sequence order."""
         from .fused import new_heads, qk_norm_rope
         total = sum(y.shape[0] for y, _, _ in segments)
-        q, k, v = new_heads(self.cfg.num_heads, total, segments[0][0].device)
+        q, k, v = new_heads(self.cfg.num_heads, padded_len(total), segments[0][0].device, valid=total)
         off = 0
         for y, qn, kn in segments:
             n = y.shape[0]
@@ -378,7 +406,8 @@ class FluxStep:
         from .fused import new_heads, qk_norm_rope
         bf16 = torch.bfloat16 if self.bf16_projections else torch.float32  # qkv feeds only the fused pass
         lt, H = txt.shape[0], self.cfg.num_heads
-        q, k, v = new_heads(H, lt + img.shape[0], img.device)
+        total = lt + img.shape[0]
+        q, k, v = new_heads(H, padded_len(total), img.device, valid=total)
         main = torch.cuda.current_stream(img.device)
         aux = aux_stream(img.device)
         aux.wait_stream(main)
@@ -392,7 +421,7 @@ class FluxStep:
         qk_norm_rope(iy, H, self.p.dense[p + "img_attn.norm.query_norm.scale"],
                      self.p.dense[p + "img_attn.norm.key_norm.scale"], cos[lt:], sin[lt:], q, k, v, lt)
         main.wait_stream(aux)
-        a = self.attn(q, k, v)
+        a = self._attn_padded(q, k, v, total)
         t_att, i_att = a[:lt], a[lt:]
         aux.wait_stream(main)
         with torch.cuda.stream(aux):
@@ -418,7 +447,8 @@ class FluxStep:
         y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=y_dtype)
         L, h = x.shape[0], cfg.hidden_size
         if self._fused(x):
-            a = self.attn(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")], cos, sin))
+            a = self._attn_padded(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")],
+                                                     cos, sin), L)
         else:
             qkv = y[:, :3 * h].reshape(L, 3, cfg.num_heads, cfg.head_dim)
             q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[p + "norm.query_norm.scale"])

@@ -47,10 +47,16 @@ def gelu_tanh_bf16(src, out):
     return out
 
 
-def new_heads(heads: int, l_total: int, device):
-    """Empty bf16 q, k, v buffers [heads, l_total, 128] for qk_norm_rope."""
+def new_heads(heads: int, l_total: int, device, valid=None):
+    """bf16 q, k, v buffers [heads, l_total, 128] for qk_norm_rope.  Rows from
+    `valid` on (padding of the joint sequence) are zero, rows before it are left
+    for qk_norm_rope to fill."""
     import torch
-    return tuple(torch.empty((heads, l_total, HEAD_DIM), dtype=torch.bfloat16, device=device) for _ in range(3))
+    bufs = tuple(torch.empty((heads, l_total, HEAD_DIM), dtype=torch.bfloat16, device=device) for _ in range(3))
+    if valid is not None and valid < l_total:
+        for t in bufs:
+            t[:, valid:].zero_()
+    return bufs
 
 
 def qk_norm_rope(qkv, heads: int, q_weight, k_weight, cos, sin, q_out, k_out, v_out, row_off: int,

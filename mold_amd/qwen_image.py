@@ -55,7 +55,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
-from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, silu
+from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, padded_len, silu
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
 MAX_PERIOD = 10000.0
@@ -295,9 +295,10 @@ class QwenImageStep:
         lt = txt.shape[0]
         fused = self._fused(img)
         heads = None
+        total = lt + img.shape[0]
         if fused:
             from .fused import new_heads
-            heads = new_heads(self.cfg.num_attention_heads, lt + img.shape[0], img.device)
+            heads = new_heads(self.cfg.num_attention_heads, padded_len(total), img.device, valid=total)
         if aux is None:
             tqkv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin, heads)
         else:
@@ -324,8 +325,10 @@ class QwenImageStep:
             iq, ik = apply_rope(iq, img_cos, img_sin), apply_rope(ik, img_cos, img_sin)
         if aux is not None:
             main.wait_stream(aux)
-        if fused:
-            a = self.attn(*heads)
+        if fused and self.attn is attention_bf16:
+            a = attention_bf16(*heads, valid=total)
+        elif fused:
+            a = self.attn(*(t[:, :total] for t in heads))
         else:
             tq, tk, tv = tqkv
             a = self.attn(torch.cat([tq, iq], dim=1), torch.cat([tk, ik], dim=1), torch.cat([tv, iv], dim=1))

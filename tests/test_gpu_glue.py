@@ -106,6 +106,28 @@ def test_gelu_tanh_bf16_matches_reference(rows, cols, lds, ldd, off, dtype):
     assert bool((dst[:, :ldd - cols] == 5.0).all())
 
 
+@pytest.mark.parametrize("valid,padded", [(295, 512), (1000, 1024), (512, 512)])
+def test_padded_attention_matches_reference(valid, padded):
+    """attention_bf16 over joint buffers padded with zero k / v rows (the fused paths pad the
+    sequence to a multiple of 256): the log-sum-exp correction removes the zero keys exactly,
+    so the result matches f32 attention on the valid rows to bf16 accuracy."""
+    from mold_amd.flux import attention_bf16
+    print(f"[case] padded attention valid={valid} padded={padded}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(valid)
+    H, D = 4, 128
+    q, k, v = (torch.randn((H, padded, D), device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+    k[:, valid:] = 0
+    v[:, valid:] = 0
+    q[:, valid:] = 3.0  # pad query rows are never read back
+    out = attention_bf16(q, k, v, valid)
+    qf, kf, vf = (t[:, :valid].float() for t in (q, k, v))
+    ref = torch.softmax(qf @ kf.transpose(1, 2) / np.sqrt(D), dim=-1) @ vf
+    ref = ref.transpose(0, 1).reshape(valid, H * D)
+    assert out.shape == (valid, H * D)
+    err = ((out.float() - ref).norm() / ref.norm()).item()
+    assert err < 5e-3, err
+
+
 def test_glue_errors_are_reported():
     mold_amd.load()
     y = torch.zeros((4, 3 * 128), device="cuda")
