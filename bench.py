@@ -244,7 +244,8 @@ def bench_qwen(dev, args):
            "weight_bytes": params.quantized_bytes(), "attention": ATTENTION_BACKEND["name"],
            "config": f"Qwen-Image shape, 1328x1328, batch 1, {l_img} img + 256 txt tokens, 60 blocks; "
                      "q/k/v Q3_K (stacked per stream), MLP Q2_K, out-projections, modulation, stems Q4_K; "
-                     "f32 residuals, bf16 GEMM inputs and attention, text stream on a second HIP stream"}
+                     "f32 residuals, bf16 GEMM inputs and attention (joint sequence padded to a multiple of 256 "
+                     "with zero keys, removed exactly), text stream on a second HIP stream"}
     return res, params, inp
 
 
