@@ -261,8 +261,12 @@ def attention_bf16(q, k, v, valid: Optional[int] = None):
             if valid < l:
                 out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
                                                                                   True)[:2]
-                fac = 1.0 / (1.0 - (l - valid) * torch.exp(-lse[0, :, :valid]))
-                o = (out[0, :, :valid].float() * fac[..., None]).to(torch.bfloat16)
+                fac = 1.0 / (1.0 - (l - valid) * torch.exp(-lse[0, :, :valid]))  # [h, valid] f32
+                # one pass: correct in f32, round to bf16, write the [valid, h, d] layout
+                res = torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device)
+                torch.mul(out[0, :, :valid].transpose(0, 1), fac.transpose(0, 1)[..., None], out=res)
+                ATTENTION_BACKEND["name"] = "fused"
+                return res.reshape(valid, h * d)
             else:
                 with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                     o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
