@@ -505,7 +505,7 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
                                                                int full_tiles, int tiles_n, int64_t m, int64_t n,
                                                                OUT *__restrict__ y, int64_t ldy,
                                                                const float *__restrict__ bias,
-                                                               const float *__restrict__ gate, int act) {
+                                                               const float *__restrict__ gate, int act, int vec) {
   const int tl = blockIdx.y;                            // tail tile
   const int idx = blockIdx.x * 256 + threadIdx.x;       // 0 .. 256 * 64 - 1
   const int r = idx >> 6, c = (idx & 63) * 4;
@@ -532,6 +532,31 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
   }
   const float sv[4] = {s.x, s.y, s.z, s.w};
   OUT *yr = y + row * ldy + col0;
+  if (vec && col0 + 3 < n) {
+    // y, bias and gate rows are 16-byte aligned here (8 for bf16 y): one
+    // vector access each
+    float o[4];
+    const float4 bv = bias ? *reinterpret_cast<const float4 *>(bias + col0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    o[0] = apply_act(sv[0] + bv.x, act);
+    o[1] = apply_act(sv[1] + bv.y, act);
+    o[2] = apply_act(sv[2] + bv.z, act);
+    o[3] = apply_act(sv[3] + bv.w, act);
+    if constexpr (std::is_same_v<OUT, float>) {
+      float4 *yv = reinterpret_cast<float4 *>(yr);
+      if (gate) {
+        const float4 rv = *yv;
+        const float4 gv = *reinterpret_cast<const float4 *>(gate + col0);
+        *yv = make_float4(__builtin_fmaf(gv.x, o[0], rv.x), __builtin_fmaf(gv.y, o[1], rv.y),
+                          __builtin_fmaf(gv.z, o[2], rv.z), __builtin_fmaf(gv.w, o[3], rv.w));
+      } else {
+        *yv = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+      __bf16 h[4] = {(__bf16)o[0], (__bf16)o[1], (__bf16)o[2], (__bf16)o[3]};
+      *reinterpret_cast<uint2 *>(yr) = *reinterpret_cast<const uint2 *>(h);
+    }
+    return;
+  }
   if constexpr (std::is_same_v<OUT, float>) {
     if (gate) {
       // the four residual values are read before any is written
@@ -573,12 +598,15 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
                          partial);
     if (split) {
       const dim3 rgrid(kBM * kBN / 4 / 256, (unsigned)(grid - full));
+      const uintptr_t ya = y_type == F32 ? 15 : 7;
+      const int vec = (reinterpret_cast<uintptr_t>(y) & ya) == 0 && ldy % 4 == 0 &&
+                      (reinterpret_cast<uintptr_t>(bias) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
       if (y_type == F32)
         hipLaunchKernelGGL(gemm_tail_reduce_kernel<float>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n, m,
-                           n, static_cast<float *>(y), ldy, bias, gate, act);
+                           n, static_cast<float *>(y), ldy, bias, gate, act, vec);
       else
         hipLaunchKernelGGL(gemm_tail_reduce_kernel<__bf16>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
-                           m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act);
+                           m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act, vec);
     }
   } else if (y_type == F32) {
     hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
