@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + mb * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
         if (row < m)
-          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act), gate, g);
+          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, act_out<OUT>(acc[mb][nb][e] + bv, act), gate, g);
       }
     }
   }
@@ -492,7 +492,7 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
       for (int e = 0; e < 16; ++e) {
         const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
         if (row < m)
-          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, apply_act(acc[mb][nb][e] + bv, act), gate, g);
+          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, act_out<OUT>(acc[mb][nb][e] + bv, act), gate, g);
       }
     }
   }
@@ -537,10 +537,10 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
     // vector access each
     float o[4];
     const float4 bv = bias ? *reinterpret_cast<const float4 *>(bias + col0) : make_float4(0.f, 0.f, 0.f, 0.f);
-    o[0] = apply_act(sv[0] + bv.x, act);
-    o[1] = apply_act(sv[1] + bv.y, act);
-    o[2] = apply_act(sv[2] + bv.z, act);
-    o[3] = apply_act(sv[3] + bv.w, act);
+    o[0] = act_out<OUT>(sv[0] + bv.x, act);
+    o[1] = act_out<OUT>(sv[1] + bv.y, act);
+    o[2] = act_out<OUT>(sv[2] + bv.z, act);
+    o[3] = act_out<OUT>(sv[3] + bv.w, act);
     if constexpr (std::is_same_v<OUT, float>) {
       float4 *yv = reinterpret_cast<float4 *>(yr);
       if (gate) {
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (col0 + j < n) store_out<OUT>(yr + j, apply_act(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
+    if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
 }
 
 template <int T>

@@ -74,4 +74,20 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
+// The same GELU-tanh for bf16 outputs: 0.5 v (1 + tanh u) = v / (1 + e^(-2u)),
+// evaluated with the hardware exponential and reciprocal (relative error about
+// 1e-6, far below bf16's 2^-8 rounding step).  f32 outputs keep apply_act.
+template <typename OUT>
+__device__ __forceinline__ float act_out(float v, int act) {
+  if constexpr (std::is_same_v<OUT, __bf16>) {
+    if (act == 1) {
+      const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+      return v * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * u));
+    }
+    return v;
+  } else {
+    return apply_act(v, act);
+  }
+}
+
 }  // namespace mq
