@@ -147,8 +147,8 @@ __global__ __launch_bounds__(256) void gelu_bf16_kernel(const IN *__restrict__ s
   if (c >= cols4) return;
   for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
     const float4 v = load4(src + r * lds + 4 * c);
-    dst[r * ldd4 + c] = make_uint2(pack_bf16x2(apply_act(v.x, 1), apply_act(v.y, 1)),
-                                   pack_bf16x2(apply_act(v.z, 1), apply_act(v.w, 1)));
+    dst[r * ldd4 + c] = make_uint2(pack_bf16x2(act_out<__bf16>(v.x, 1), act_out<__bf16>(v.y, 1)),
+                                   pack_bf16x2(act_out<__bf16>(v.z, 1), act_out<__bf16>(v.w, 1)));
   }
 }
 
