@@ -185,9 +185,9 @@ int run_gemm(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64
     a = st;
     lda = kp;
   }
-  GemmTail tail = gemm_tail_plan(m, n, k, ctx->cu_count);
+  GemmTail tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
   float *partial = nullptr;
-  if (tail.kparts > 1 && gemm_fast_ok(m, k, lda)) partial = tail_buffer(ctx, s, gemm_tail_bytes(tail, m, n));
+  if (tail.kparts > 1 && gemm_fast_ok(w->dtype, m, k, lda)) partial = tail_buffer(ctx, s, gemm_tail_bytes(tail, m, n));
   hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, tail,
                              partial, s);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");

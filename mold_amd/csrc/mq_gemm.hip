@@ -1,26 +1,34 @@
 // mq_gemm.hip — fused dequant -> bf16 MFMA GEMM for large-M quantized linears
 // (FLUX / Qwen-Image token projections): y[m, n] = act(x[m, :] . W[n, :] + b[n]).
 //
-// Both kernels tile for gfx950 (256 CUs in 8 XCDs, 64-wide waves, 160 KiB
-// LDS per CU) the same way:
-//   * workgroup = 4 waves (one per SIMD), block tile 256 (m) x 256 (n);
-//   * wave w owns weight tile nt*4 + w (64 output features) for all 256 rows,
-//     so every weight element is decoded exactly once per block tile and goes
-//     straight from registers into the MFMA B operand (no LDS round trip);
-//   * the bf16 activation tile is staged through LDS (XOR-swizzled 16-byte
-//     chunks, one barrier per K step of 64) and read by all four waves;
-//   * v_mfma_f32_32x32x16_bf16: per wave 8 (m) x 2 (n) accumulator tiles,
-//     256 f32 accumulators per lane;
-//   * blockIdx -> tile mapping gives each XCD a contiguous range of tiles that
-//     share the same activation panel in its L2.
-// gemm_fast_kernel (k a multiple of 256) decodes with the per-type fragment
-// decoders of mq_bfrag.h and pipelines loads, decode and MFMAs; gemm_kernel
-// handles any k with the generic 8-element decoder.
-// Within a K step of 64, lane half h (lane / 32) supplies K elements
-// {16h..16h+15} u {32+16h..32+16h+15} (four runs of 8) in gemm_kernel, and
-// the per-type chunk order TT::chunk(s, h) in gemm_fast_kernel; the A operand
-// reads the same runs from LDS, so the K order inside a step is a permutation
-// shared by both operands.
+// gemm_fast_kernel (k a whole number of the weight type's K units) is the
+// path every BASELINE shape takes.  It is shaped for gfx950's CUs (4 SIMDs,
+// 512 VGPRs per SIMD lane, 160 KiB LDS) so that TWO workgroups share each CU:
+//   * workgroup = 4 waves (one per SIMD), block tile 256 (m) x 128 (n); with
+//     two workgroups per CU every SIMD holds two waves, so one wave's MFMAs
+//     run while the other decodes weights, and one workgroup's epilogue,
+//     prologue and memory waits overlap the other's main loop;
+//   * wave w owns output features 32w .. 32w+31 of the tile for all 256
+//     rows: lane (l32, h) decodes weight row l32 of that run straight into
+//     the MFMA B operand (per-type decoders, mq_bfrag.h), so every weight is
+//     decoded once per block tile and B never touches LDS;
+//   * v_mfma_f32_32x32x16_bf16, 8 accumulator tiles (128 f32) per lane;
+//   * the bf16 activation tile (256 x 64 per K step) goes global -> VGPR ->
+//     LDS one step ahead through a 2-slot ring (2 x 32 KiB per workgroup),
+//     with buffer loads whose range check turns rows past m into zeros;
+//     every memory operation is visible to the compiler, so its waits are
+//     exact and loads stay in flight across the step barrier;
+//   * rows are 128 B, chunk c of row r in slot c ^ ((r >> 1) & 7), so the
+//     16 lanes of a ds_read_b128 / ds_write_b128 quarter hit distinct banks;
+//   * XCD-aware tile order: workgroup i runs on XCD i % 8; each XCD gets a
+//     contiguous run of tiles, row-major over n, so the tiles in flight on
+//     one XCD share the activation panel in its L2.
+// gemm_kernel handles any k with the generic 8-element decoder (256 x 256
+// tiles, one workgroup per CU).
+// Within a K step of 64, lane half h (lane / 32) supplies the per-type chunk
+// order TT::chunk(s, h) (gemm_kernel: K elements {16h..16h+15} u
+// {32+16h..32+16h+15}); the A operand reads the same runs from LDS, so the K
+// order inside a step is a permutation shared by both operands.
 #include <type_traits>
 #include <utility>
 
@@ -196,63 +204,36 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
   }
 }
 
-constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
+// ---------------------------------------------------------------------------
+// Fast path.  Block tile kFM x kFN, K step kFK; see the file comment.
+constexpr int kFM = kGemmTileM, kFN = kGemmTileN, kFK = 64;
 constexpr int kFastThreads = 256;
-typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
 
-// One 1 KiB direct global->LDS load: lane i's 16 bytes from g land at LDS byte
-// address lds + 16 i.  Issued as inline asm so that the compiler does not see
-// an LDS write it cannot tell apart from the slot being read (it would wait
-// for every outstanding load before each LDS access, which turns the two-step
-// A prefetch into none); the kernel orders these loads with its own
-// s_waitcnt at the step barrier.  The compiler's waits for its own loads then
-// count fewer outstanding loads than there are, so they can only wait longer
-// than needed, never shorter.  M0 carries the LDS address (no other code in
-// these kernels uses M0); s_nop: one wait state between writing M0 and the
-// LDS-DMA instruction that reads it.
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+// Raw buffer resource over `bytes` bytes at p (gfx9 untyped buffer: loads
+// past `bytes` return 0 and stores past it are dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// ---------------------------------------------------------------------------
-// Fast path (k a multiple of the type's unit, 16-byte aligned activation
-// rows): one wave per SIMD, 256 x 256 block tile, 4 waves, K step 64.
-//   * wave w owns weight tile nt*4 + w (64 output features) for all 256 rows:
-//     lane (l32, h) decodes weight rows l32 and l32 + 32 of that tile straight
-//     into MFMA B operands (per-type decoders, mq_bfrag.h), so every weight
-//     is decoded once per block tile and B never touches LDS;
-//   * A (bf16 activations, 256 x 64 per step) goes global -> LDS by direct
-//     loads (dma16) into a 4-slot ring three steps ahead, one barrier per
-//     step; rows are 128 B with 16-byte chunk c of row r in slot
-//     c ^ ((r >> 1) & 7), so the 16 lanes of a ds_read_b128 quarter hit
-//     distinct banks;
-//   * with one wave per SIMD each wave has 512 registers: the 8 x 2 tiles of
-//     v_mfma_f32_32x32x16_bf16 accumulators (256 f32) sit in AGPRs, leaving
-//     room to read the next slice's A fragments and decode its B operands
-//     (the next step's first slice during the last slice) while the current
-//     slice's 16 MFMAs run;
-//   * XCD-aware tile order (workgroup i runs on XCD i % 8; each XCD gets a
-//     contiguous run of tiles, row-major over n, sharing the x panel in L2);
-//   * weight bytes for unit u+1 are fetched during unit u (one unit ahead);
-//     every load is unconditional (the last unit re-reads itself), so the
-//     compiler's wait counts are the same on every path.
+// Barrier between K steps: this wave's LDS writes and reads are complete,
+// every wave has arrived; global loads stay in flight (__syncthreads would
+// wait for them).  The memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void step_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int TYPE, typename OUT>
-__global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
+template <int TYPE, typename OUT, bool GATED>
+__global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
-    OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate,
-    const float *__restrict__ res, int act, int tiles_m, int tiles_n, int full_tiles, int kparts,
-    float *__restrict__ partial) {
+    OUT *y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate, int act, int tiles_m,
+    int tiles_n, int full_tiles, int kparts, float *__restrict__ partial) {
   using TT = bfrag::T<TYPE>;
-  constexpr int kSteps = TT::kUnitK / kBK;
-  // VALU instructions placed after each pair of MFMAs (the decode work per
-  // MFMA differs by type; measured best per type)
-  constexpr int kVpm = TYPE == Q8_0 ? 3 : (TYPE == Q4_K || TYPE == Q5_K) ? 6 : 8;
-  __shared__ uint4 lds_a[4][kBM * kBK / 8];
+  constexpr int kP = TT::kUnitK / kFK;  // K steps per weight unit
+  __shared__ uint4 lds_a[2][kFM * kFK / 8];
 
   // Workgroups 0 .. full_tiles-1 run whole tiles (XCD-aware order over
   // them); the rest run K part `part` of tail tile full_tiles + (w / kparts):
-  // the units [part * U / kparts, (part + 1) * U / kparts) of the U = k / 256,
+  // the units [part * U / kparts, (part + 1) * U / kparts) of the U = k / unit,
   // written raw to `partial` for gemm_tail_reduce_kernel.
   const int bid = blockIdx.x;
   int v, part = -1;
@@ -270,231 +251,156 @@ __global__ __launch_bounds__(kFastThreads, 1) void gemm_fast_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
-  const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
-  const int64_t m0 = (int64_t)mt * kBM;
-  const int64_t all_units = k / TT::kUnitK;
-  const int64_t ub = part < 0 ? 0 : part * all_units / kparts;                  // first unit
-  const int64_t units = part < 0 ? all_units : (part + 1) * all_units / kparts - ub;
-  const int64_t ksteps = units * kSteps;
-  a += ub * TT::kUnitK;  // A columns of this K range
-  const int64_t wt_raw = (int64_t)nt * (kBN / kRowTile) + wave;
+  const int64_t m0 = (int64_t)mt * kFM;
+  const int64_t c0 = (int64_t)nt * kFN + 32 * wave;  // this wave's first output feature
+  const int64_t wt_raw = c0 / kRowTile;              // its weight tile
+  const int wrow = (int)(c0 - wt_raw * kRowTile) + l32;  // this lane's row in that tile
   const int64_t wt = wt_raw < ntiles_w ? wt_raw : ntiles_w - 1;  // keep reads in bounds
+  const int64_t all_units = k / TT::kUnitK;
+  const int64_t ub = part < 0 ? 0 : part * all_units / kparts;  // first unit
+  const int64_t units = part < 0 ? all_units : (part + 1) * all_units / kparts - ub;
+  const int64_t ksteps = units * kP;
 
-  f32x16 acc[8][2];
+  f32x16 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
 
-  // A: 4-slot LDS ring filled by direct global->LDS loads three K steps
-  // ahead.  Load i (0..7) of wave w fills LDS rows 64w + 8i .. +7 (1 KiB);
-  // lane j fetches row 64w + 8i + j/8, logical chunk (j&7) ^ ((row>>1)&7).
-  // Rows past m read row m-1 (finite, never stored).
-  int aoff[8];
+  // A staging: thread -> 16-byte chunk ac of rows ar + 32 i (i = 0..7) of the
+  // 256 x 64 step tile, moved in two halves (i < 4, i >= 4) of four loads so
+  // that only 16 VGPRs hold A in flight.  The row's byte offset is the buffer
+  // load's voffset (range-checked: rows >= m read 0); the K offset is uniform
+  // (soffset).
+  const int ac = tid & 7, ar = tid >> 3;
+  const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(a, (uint32_t)(m * lda * 2));
+  const uint32_t avoff = (uint32_t)(((m0 + ar) * lda + ac * 8) * 2);
+  const uint32_t arow = (uint32_t)(32 * lda * 2);
+  const uint32_t akb = (uint32_t)(ub * TT::kUnitK * 2);
+  uint4 ast[4];
+  auto load_a = [&](int64_t ks, int half) {
+    const uint32_t kb = akb + (uint32_t)ks * (kFK * 2);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 64 * wave + 8 * i + (lane >> 3);
-    int64_t row = m0 + r;
-    row = row < m ? row : m - 1;
-    aoff[i] = (int)(row * lda + (((lane & 7) ^ ((r >> 1) & 7)) * 8));
-  }
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto dma_a = [&](uint4 *slot, int64_t ks) {
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_void_t *)(slot + 64 * 8 * wave_u);
+    for (int i = 0; i < 4; ++i) {
+      auto t = __builtin_amdgcn_raw_buffer_load_b128(arsrc, avoff + (4 * half + i) * arow, kb, 0);
+      __builtin_memcpy(&ast[i], &t, 16);
+    }
+  };
+  const int sw_st = ac ^ ((ar >> 1) & 7);  // (ar + 32 i) >> 1 & 7 == ar >> 1 & 7
+  auto store_a = [&](int slot, int half) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dma16(a + aoff[i] + ks * kBK, dst + 1024 * i);
+    for (int i = 0; i < 4; ++i) lds_a[slot][(ar + 32 * (4 * half + i)) * 8 + sw_st] = ast[i];
+  };
+  const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
+  auto read_a = [&](int slot, int mb, int S) -> bf16x8 {
+    const char *p = reinterpret_cast<const char *>(lds_a[slot]) + l32 * 128 + ((TT::chunk(S, h) ^ swz) << 4) +
+                    mb * 4096;
+    return *reinterpret_cast<const bf16x8 *>(p);
   };
 
-  typename TT::Raw raw[2];
-  typename TT::Sc sc[2];
-  // Barrier between K steps (global loads stay in flight across it, which
-  // __syncthreads would not allow).  At the end of step ks the A loads for step ks+1 (issued two steps
-  // earlier) must have landed; younger than them are at least the 16 loads
-  // for steps ks+2 and ks+3, so vmcnt(16) suffices and leaves the newest
-  // weight reloads in flight.
-  auto step_sync = [&]() { asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-
-  // A fragments of slice S from slot `slot`, and B operands of slice S of
-  // step G from the unpacked weight bytes.
-  bf16x8 af[2][8], bf[2][2];
-  auto read_a = [&](bf16x8 *dst, const uint4 *__restrict__ slot, int S) {
-    const char *abase = reinterpret_cast<const char *>(slot) + l32 * 128 + (TT::chunk(S, h) ^ swz) * 16;
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) dst[mb] = *reinterpret_cast<const bf16x8 *>(abase + mb * 4096);
-  };
-  auto decode_b = [&]<int G, int S>(bf16x8 *dst) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) dst[j] = TT::template frag<G, S>(raw[j], sc[j]);
-  };
-
-  // prologue: unit 0's weight bytes and scales, A(0) and A(1) into slots 0, 1;
-  // step 0's slice-0 operands
-#pragma unroll
-  for (int j = 0; j < 2; ++j) TT::load_prep(raw[j], w, wt, l32 + 32 * j, ub, h);
-  static_for<kSteps>([&]<int G>() {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, ub, h);
-  });
-  dma_a(lds_a[0], 0);
-  dma_a(lds_a[1], ksteps > 1 ? 1 : 0);
-  dma_a(lds_a[2], ksteps > 2 ? 2 : ksteps - 1);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) TT::prep(raw[j], sc[j], h);
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  read_a(af[0], lds_a[0], 0);
-  decode_b.template operator()<0, 0>(bf[0]);
+  typename TT::Raw raw;
+  typename TT::Sc sc;
+  // prologue: unit 0's weight bytes and scales, A(0) into slot 0
+  TT::load_prep(raw, w, wt, wrow, ub, h);
+  static_for<kP>([&]<int G>() { TT::template reload<G>(raw, w, wt, wrow, ub, h); });
+  load_a(0, 0);
+  store_a(0, 0);
+  load_a(0, 1);
+  store_a(0, 1);
+  TT::prep(raw, sc, h);
+  step_barrier();
 
   for (int64_t u = 0; u < units; ++u) {
-    const int64_t un = u + 1 < units ? u + 1 : u;
-    static_for<kSteps>([&]<int G>() {
-      const int64_t ks = u * kSteps + G;
-      const int64_t kf = ks + 3 < ksteps ? ks + 3 : ksteps - 1;
-      auto body = [&](const uint4 *__restrict__ a_cur, const uint4 *__restrict__ a_next,
-                      uint4 *__restrict__ a_fill) {
-        dma_a(a_fill, kf);
-        static_for<4>([&]<int S>() {
-          // operands of the next slice (slice 0 of the next step after S = 3)
-          if constexpr (S < 3) {
-            read_a(af[(S + 1) & 1], a_cur, S + 1);
-            decode_b.template operator()<G, S + 1>(bf[(S + 1) & 1]);
-          } else {
-            // piece G is fully decoded: fetch unit u+1's (and its scale bytes
-            // after step 0); unit u+1's scales are unpacked before its first
-            // slice is decoded.
+    const int64_t un = u + 1 < units ? u + 1 : u;  // the last unit re-reads itself
+    static_for<kP>([&]<int G>() {
+      const int64_t ks = u * kP + G;
+      const int64_t kn = ks + 1 < ksteps ? ks + 1 : ks;  // the last step re-reads itself
+      const int slot = (int)(ks & 1);
+      // A(ks+1) goes into the other slot (read last in step ks-1), in two
+      // halves: the first half's loads are in flight during slices 0-1, the
+      // second's during slices 2-3
+      load_a(kn, 0);
+      bf16x8 bf[2];
+      bf[0] = TT::template frag<G, 0>(raw, sc);
+      static_for<4>([&]<int S>() {
+        if constexpr (S < 3) bf[(S + 1) & 1] = TT::template frag<G, S + 1>(raw, sc);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              TT::template reload<G>(raw[j], w, wt, l32 + 32 * j, ub + un, h);
-              if constexpr (G == 0) TT::load_prep(raw[j], w, wt, l32 + 32 * j, ub + un, h);
-            }
-            read_a(af[0], a_next, 0);
-            if constexpr (G + 1 < kSteps) {
-              decode_b.template operator()<G + 1, 0>(bf[0]);
-            } else {
-#pragma unroll
-              for (int j = 0; j < 2; ++j) TT::prep(raw[j], sc[j], h);
-              decode_b.template operator()<0, 0>(bf[0]);
-            }
-          }
-#pragma unroll
-          for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-              acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[S & 1][mb], bf[S & 1][nb], acc[mb][nb], 0,
-                                                                    0, 0);
-          static_for<8>([&]<int I>() {
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, kVpm, 0);
-          });
-        });
-      };
-      body(lds_a[ks & 3], lds_a[(ks + 1) & 3], lds_a[(ks + 3) & 3]);
-      step_sync();
+        for (int mb = 0; mb < 8; ++mb)
+          acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_a(slot, mb, S), bf[S & 1], acc[mb], 0, 0, 0);
+        if constexpr (S == 1) {
+          store_a(slot ^ 1, 0);
+          load_a(kn, 1);
+        }
+      });
+      // piece G of unit u is fully decoded: fetch it for unit u+1 (and, after
+      // step 0, unit u+1's scale bytes, unpacked after its last step)
+      TT::template reload<G>(raw, w, wt, wrow, ub + un, h);
+      if constexpr (G == 0) TT::load_prep(raw, w, wt, wrow, ub + un, h);
+      if constexpr (G == kP - 1) TT::prep(raw, sc, h);
+      store_a(slot ^ 1, 1);
+      step_barrier();
     });
   }
 
-  // no A load may still be in flight when the wave ends
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // ---- epilogue: lane holds column l32 of each 32x32 tile, rows
-  // 8*(e/4) + 4*h + (e%4).
-  if (wt_raw >= ntiles_w) return;
+  // ---- epilogue: lane holds output feature c0 + l32 of each 32 x 32 tile mb,
+  // rows 8*(e/4) + 4*h + (e%4).
+  if (c0 >= n) return;
   if (part >= 0) {
-    // raw sums of this K part: tile-local row-major [256][256] f32 block
-    float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kBM * kBN) + 4 * h * kBN + wave * 64 + l32;
+    // raw sums of this K part: tile-local row-major [256][128] f32 block
+    float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kFM * kFN) + 4 * h * kFN + 32 * wave + l32;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kFN] = acc[mb][e];
+    return;
+  }
+  const int64_t col = c0 + l32;
+  const int64_t row0 = m0 + 4 * h;
+  const bool colok = col < n;
+  const float bv = bias && colok ? bias[col] : 0.f;
+  OUT *yc = y + row0 * ldy + col;
+  if constexpr (GATED) {
+    // y = y + g * v: block mb + 1's residual rows are loaded before block mb
+    // is stored (one memory latency per tile column, not one per element);
+    // rows past m and columns past n are neither read nor written
+    const float g = colok ? gate[col] : 0.f;
+    float r[2][16];
+    auto load_block = [&](int mb, float *dst) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
+        dst[e] = colok && row0 + ro < m ? yc[ro * ldy] : 0.f;
+      }
+    };
+    load_block(0, r[0]);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      if (mb + 1 < 8) load_block(mb + 1, r[(mb + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
+        if (colok && row0 + ro < m) yc[ro * ldy] = __builtin_fmaf(g, apply_act(acc[mb][e] + bv, act), r[mb & 1][e]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  } else {
+    if (m0 + kFM <= m && c0 + 32 <= n && act == MQ_ACT_NONE_) {
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kBN + nb * 32] = acc[mb][nb][e];
-    return;
-  }
-  const int64_t row0 = m0 + 4 * h;
-  const int64_t col0 = wt_raw * kRowTile + l32;
-  if (m0 + kBM <= m && wt_raw * kRowTile + kRowTile <= n && act == MQ_ACT_NONE_) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const float bv = bias ? bias[col0 + nb * 32] : 0.f;
-      OUT *yc = y + row0 * ldy + col0 + nb * 32;
-      if constexpr (std::is_same_v<OUT, float>) {
-        if (gate) {
-          // residual rows of 32-row block mb + 1 are loaded before block mb is
-          // stored: one memory latency per tile column, not one per element
-          const float g = gate[col0 + nb * 32];
-          const float *rc = res + row0 * ldy + col0 + nb * 32;
-          float r[2][16];
-#pragma unroll
-          for (int e = 0; e < 16; ++e) r[0][e] = rc[(8 * (e >> 2) + (e & 3)) * ldy];
-#pragma unroll
-          for (int mb = 0; mb < 8; ++mb) {
-            if (mb + 1 < 8) {
-#pragma unroll
-              for (int e = 0; e < 16; ++e) r[(mb + 1) & 1][e] = rc[((mb + 1) * 32 + 8 * (e >> 2) + (e & 3)) * ldy];
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-              yc[(mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy] = __builtin_fmaf(g, acc[mb][nb][e] + bv, r[mb & 1][e]);
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          continue;
-        }
-      }
-      {
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][nb][e] + bv);
-      }
+        for (int e = 0; e < 16; ++e) store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
+      return;
     }
-    return;
-  }
+    if (!colok) return;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int64_t col = col0 + nb * 32;
-    if (col >= n) continue;
-    const float bv = bias ? bias[col] : 0.f;
-    const float g = gate ? gate[col] : 0.f;
-    if constexpr (std::is_same_v<OUT, float>) {
-      if (gate) {
-        // as the full-tile path: block mb + 1's residual rows loaded before
-        // block mb is stored; rows past m are neither read nor written
-        float r[2][16];
-        auto load_block = [&](int mb, float *dst) {
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
-            dst[e] = row < m ? res[row * ldy + col] : 0.f;
-          }
-        };
-        load_block(0, r[0]);
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-          if (mb + 1 < 8) load_block(mb + 1, r[(mb + 1) & 1]);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
-            if (row < m) y[row * ldy + col] = __builtin_fmaf(g, apply_act(acc[mb][nb][e] + bv, act), r[mb & 1][e]);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        continue;
-      }
-    }
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
+    for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int64_t row = row0 + mb * 32 + 8 * (e >> 2) + (e & 3);
-        if (row < m)
-          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, act_out<OUT>(acc[mb][nb][e] + bv, act), gate, g);
+        const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
+        if (row0 + ro < m) store_out<OUT>(yc + ro * ldy, act_out<OUT>(acc[mb][e] + bv, act));
       }
-    }
   }
 }
 
@@ -506,20 +412,20 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
                                                                OUT *__restrict__ y, int64_t ldy,
                                                                const float *__restrict__ bias,
                                                                const float *__restrict__ gate, int act, int vec) {
-  const int tl = blockIdx.y;                            // tail tile
-  const int idx = blockIdx.x * 256 + threadIdx.x;       // 0 .. 256 * 64 - 1
-  const int r = idx >> 6, c = (idx & 63) * 4;
+  const int tl = blockIdx.y;                                  // tail tile
+  const int idx = blockIdx.x * 256 + threadIdx.x;             // 0 .. kFM * kFN / 4 - 1
+  const int r = idx / (kFN / 4), c = (idx % (kFN / 4)) * 4;
   const int v = full_tiles + tl;
   const int mt = v / tiles_n, nt = v - mt * tiles_n;
-  const int64_t row = (int64_t)mt * kBM + r, col0 = (int64_t)nt * kBN + c;
+  const int64_t row = (int64_t)mt * kFM + r, col0 = (int64_t)nt * kFN + c;
   if (row >= m) return;
-  const float *src = partial + (int64_t)tl * kparts * (kBM * kBN) + r * kBN + c;
+  const float *src = partial + (int64_t)tl * kparts * (kFM * kFN) + r * kFN + c;
   // every part's load is issued before the first add (no chain of
   // latencies), then the parts are added in order
   float4 t[kGemmMaxKParts];
 #pragma unroll
   for (int p = 0; p < kGemmMaxKParts; ++p)
-    if (p < kparts) t[p] = *reinterpret_cast<const float4 *>(src + (int64_t)p * (kBM * kBN));
+    if (p < kparts) t[p] = *reinterpret_cast<const float4 *>(src + (int64_t)p * (kFM * kFN));
   float4 s = t[0];
 #pragma unroll
   for (int p = 1; p < kGemmMaxKParts; ++p) {
@@ -575,29 +481,38 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
     if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
 }
 
+template <typename OUT, bool GATED>
+static void launch_fast(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
+                        int64_t lda, void *y, int64_t ldy, const float *bias, const float *gate, int act,
+                        int tiles_m, int tiles_n, int full, int kp, float *partial, int wgs, hipStream_t stream) {
+  hipLaunchKernelGGL((gemm_fast_kernel<MQ_GEMM_TYPE, OUT, GATED>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n,
+                     k, ntiles_w, a, m, lda, static_cast<OUT *>(y), ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
+                     partial);
+}
+
 template <int T>
 hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                             int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
                             int act, const GemmTail &tail, float *partial, hipStream_t stream) {
-  const int tiles_m = (int)((m + kBM - 1) / kBM);
-  const int tiles_n = (int)((n + kBN - 1) / kBN);
-  const int grid = tiles_m * tiles_n;
-  const float *res = gate ? static_cast<const float *>(y) : nullptr;  // the gated update reads y, then writes it
-  if (gemm_fast_ok(m, k, lda)) {
+  if (gemm_fast_ok(T, m, k, lda)) {
+    const int tiles_m = (int)((m + kFM - 1) / kFM);
+    const int tiles_n = (int)((n + kFN - 1) / kFN);
+    const int grid = tiles_m * tiles_n;
     const bool split = partial && tail.kparts > 1;
     const int full = split ? tail.full_tiles : grid;
     const int kp = split ? tail.kparts : 1;
     const int wgs = full + (grid - full) * kp;
-    if (y_type == F32)
-      hipLaunchKernelGGL((gemm_fast_kernel<T, float>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n, k, ntiles_w, a,
-                         m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n, full, kp,
-                         partial);
+    if (gate)
+      launch_fast<float, true>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
+                               partial, wgs, stream);
+    else if (y_type == F32)
+      launch_fast<float, false>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
+                                kp, partial, wgs, stream);
     else
-      hipLaunchKernelGGL((gemm_fast_kernel<T, __bf16>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n, k, ntiles_w,
-                         a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n, full, kp,
-                         partial);
+      launch_fast<__bf16, false>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
+                                 kp, partial, wgs, stream);
     if (split) {
-      const dim3 rgrid(kBM * kBN / 4 / 256, (unsigned)(grid - full));
+      const dim3 rgrid(kFM * kFN / 4 / 256, (unsigned)(grid - full));
       const uintptr_t ya = y_type == F32 ? 15 : 7;
       const int vec = (reinterpret_cast<uintptr_t>(y) & ya) == 0 && ldy % 4 == 0 &&
                       (reinterpret_cast<uintptr_t>(bias) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
@@ -608,13 +523,18 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
         hipLaunchKernelGGL(gemm_tail_reduce_kernel<__bf16>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
                            m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act, vec);
     }
-  } else if (y_type == F32) {
-    hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
-                       a, m, lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
-  } else {
-    hipLaunchKernelGGL((gemm_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w,
-                       a, m, lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
+    return hipGetLastError();
   }
+  const int tiles_m = (int)((m + kBM - 1) / kBM);
+  const int tiles_n = (int)((n + kBN - 1) / kBN);
+  const int grid = tiles_m * tiles_n;
+  const float *res = gate ? static_cast<const float *>(y) : nullptr;  // the gated update reads y, then writes it
+  if (y_type == F32)
+    hipLaunchKernelGGL((gemm_kernel<T, float>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w, a, m,
+                       lda, static_cast<float *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
+  else
+    hipLaunchKernelGGL((gemm_kernel<T, __bf16>), dim3(grid), dim3(kGemmThreads), 0, stream, w, n, k, ntiles_w, a, m,
+                       lda, static_cast<__bf16 *>(y), ldy, bias, gate, res, act, tiles_m, tiles_n);
   return hipGetLastError();
 }
 
@@ -624,13 +544,17 @@ template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64
 
 #else  // the type dispatcher
 
-GemmTail gemm_tail_plan(int64_t m, int64_t n, int64_t k, int cus) {
-  const int64_t tiles = ((m + kGemmTile - 1) / kGemmTile) * ((n + kGemmTile - 1) / kGemmTile);
-  const int64_t rem = tiles % cus;                 // tiles of the last, partial round
-  const int64_t units = k / 256;
+// Tail plan of the fast kernel: when the last round of tiles over the CUs'
+// workgroup slots is partial, split each of those tail tiles into kp K parts
+// so that they fill one round.
+GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus) {
+  const int64_t tiles = ((m + kGemmTileM - 1) / kGemmTileM) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int64_t slots = (int64_t)cus * kGemmWgsPerCu;
+  const int64_t rem = tiles % slots;  // tiles of the last, partial round
+  const int64_t units = k / gemm_unit_k(type);
   GemmTail t{(int)tiles, 1};
   if (rem == 0 || units < 2) return t;
-  int64_t kp = cus / rem;                          // K parts per tail tile: they fill one round
+  int64_t kp = slots / rem;  // K parts per tail tile: they fill one round
   kp = kp < units ? kp : units;
   kp = kp < kGemmMaxKParts ? kp : kGemmMaxKParts;
   if (kp < 2) return t;
@@ -640,9 +564,9 @@ GemmTail gemm_tail_plan(int64_t m, int64_t n, int64_t k, int cus) {
 }
 
 size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n) {
-  const int64_t tiles = ((m + kGemmTile - 1) / kGemmTile) * ((n + kGemmTile - 1) / kGemmTile);
+  const int64_t tiles = ((m + kGemmTileM - 1) / kGemmTileM) * ((n + kGemmTileN - 1) / kGemmTileN);
   if (t.kparts < 2) return 0;
-  return (size_t)(tiles - t.full_tiles) * t.kparts * kGemmTile * kGemmTile * sizeof(float);
+  return (size_t)(tiles - t.full_tiles) * t.kparts * kGemmTileM * kGemmTileN * sizeof(float);
 }
 
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,

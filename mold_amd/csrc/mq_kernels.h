@@ -33,27 +33,33 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const flo
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
                        float *partial, int cus, hipStream_t stream);
 
-// Fused dequant -> LDS -> bf16 MFMA GEMM.  a is bf16 [m, lda] with lda a
-// multiple of 64 covering ceil(k/64)*64 zero-padded columns.  With `gate`
-// (f32 [n], f32 y only) the output is the gated residual update
+// Fused dequant -> bf16 MFMA GEMM.  a is bf16 [m, lda] with lda a multiple
+// of 64 covering ceil(k/64)*64 zero-padded columns.  With `gate` (f32 [n],
+// f32 y only) the output is the gated residual update
 // y = y + gate * act(a . W^T + bias); without it y = act(a . W^T + bias).
-// Tiles are 256 x 256.  When the last round of tiles over the CUs is
-// partial, those tail tiles may split K into `kparts` workgroups that write
-// raw sums to `partial` (gemm_tail_bytes of it), added in part order by a
-// second kernel that applies the epilogue: the plan comes from
-// gemm_tail_plan; partial == NULL runs every tile whole.
-constexpr int kGemmTile = 256;
+// The fast kernel (k a whole number of the type's 128- or 256-weight units)
+// runs 256 (m) x 128 (n) block tiles, two workgroups per CU.  When the last
+// round of tiles over the CUs' slots is partial, those tail tiles may split K
+// into `kparts` workgroups that write raw sums to `partial`
+// (gemm_tail_bytes of it), added in part order by a second kernel that
+// applies the epilogue: the plan comes from gemm_tail_plan; partial == NULL
+// runs every tile whole.  Other k take a generic 256 x 256 kernel.
+constexpr int kGemmTileM = 256;      // fast kernel block tile (rows of x)
+constexpr int kGemmTileN = 128;      // fast kernel block tile (output features)
+constexpr int kGemmWgsPerCu = 2;     // fast kernel workgroups resident per CU
 constexpr int kGemmMaxKParts = 8;
 struct GemmTail {
   int full_tiles;  // tiles run whole (all of them when kparts == 1)
   int kparts;      // K parts per tail tile
 };
-GemmTail gemm_tail_plan(int64_t m, int64_t n, int64_t k, int cus);
+// K unit of the fast kernel per weight type (the decoder's unit in mq_bfrag.h).
+inline int gemm_unit_k(int type) { return type == Q8_0 ? 128 : 256; }
+GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus);
 size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n);
-// The fast kernel (and tail splitting) applies: whole 256-wide K units,
-// 16-byte aligned rows and element offsets of x that fit 32 bits.
-inline bool gemm_fast_ok(int64_t m, int64_t k, int64_t lda) {
-  return (k % 256) == 0 && lda % 8 == 0 && m * lda < (int64_t(1) << 31) - 64;
+// The fast kernel (and tail splitting) applies: whole K units, 16-byte aligned
+// rows, and byte offsets of x that fit the 31-bit buffer range.
+inline bool gemm_fast_ok(int type, int64_t m, int64_t k, int64_t lda) {
+  return (k % gemm_unit_k(type)) == 0 && lda % 8 == 0 && (m + kGemmTileM) * lda * 2 < (int64_t(1) << 31);
 }
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w,
                        const __bf16 *a, int64_t m, int64_t lda, void *y, int y_type, int64_t ldy,
