@@ -429,24 +429,36 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
   const int64_t n = w->n, k = w->k;
 
   if (m <= kGemvMaxM) {
-    const float *xf = static_cast<const float *>(x);
+    if (gemv_reads_x_in_place(w->dtype, m, n, k, x, x_dtype, ldx, ctx->cu_count)) {
+      // Q4_K: f32 or bf16 x read in place, no scratch
+      hipError_t e = launch_gemv(w->dtype, wv, n, k, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, act, nullptr,
+                                 ctx->cu_count, s);
+      if (e != hipSuccess) return hip_fail(e, "gemv launch");
+      return MQ_OK;
+    }
+    // otherwise x goes to scratch as contiguous f32 (widened from bf16, or
+    // copied when its rows are not 16-byte aligned) unless it already is
+    const void *xf = x;
     int64_t ldxf = ldx;
-    size_t need = gemv_scratch_bytes(w->dtype, m, n, k);
+    const bool stage_x = x_dtype == MQ_BF16 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 || (ldx % 4) != 0;
+    size_t need = gemv_scratch_bytes(w->dtype, m, n, k, ctx->cu_count);
     size_t xoff = (need + 255) & ~size_t(255);
-    if (x_dtype == MQ_BF16) need = xoff + (size_t)m * k * sizeof(float);
+    if (stage_x) need = xoff + (size_t)m * k * sizeof(float);
     if (need) {
       int rc = ensure_scratch(ctx, need);
       if (rc) return rc;
     }
-    if (x_dtype == MQ_BF16) {
-      // widen to f32 (the GEMV reads f32 through the scalar cache)
+    if (stage_x) {
       float *xs = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + xoff);
-      hipError_t e = launch_widen_bf16(static_cast<const __bf16 *>(x), m, k, ldx, xs, s);
-      if (e != hipSuccess) return hip_fail(e, "widen bf16 activations");
+      hipError_t e = x_dtype == MQ_BF16
+                         ? launch_widen_bf16(static_cast<const __bf16 *>(x), m, k, ldx, xs, s)
+                         : hipMemcpy2DAsync(xs, k * sizeof(float), x, ldx * sizeof(float), k * sizeof(float), m,
+                                            hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) return hip_fail(e, "stage activations for the GEMV");
       xf = xs;
       ldxf = k;
     }
-    hipError_t e = launch_gemv(w->dtype, wv, n, k, xf, m, ldxf, y, y_dtype, ldy, bias, act,
+    hipError_t e = launch_gemv(w->dtype, wv, n, k, xf, MQ_F32, m, ldxf, y, y_dtype, ldy, bias, act,
                                static_cast<float *>(ctx->scratch), ctx->cu_count, s);
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return MQ_OK;

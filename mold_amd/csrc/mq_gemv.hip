@@ -1,7 +1,8 @@
 // mq_gemv.hip — skinny-M quantized GEMV, y[m, n] = x[m, :] . W[n, :] for
 // m <= 8 (FLUX/Qwen adaLN modulation, final-layer modulation: m = batch).
 //
-// HBM-bound: every weight byte is read exactly once.  Mapping: a workgroup
+// HBM-bound: every weight byte is read exactly once.  Q4_K weights take
+// gemv_q4k_kernel (below).  The generic kernel (other types): a workgroup
 // owns one 64-row weight tile and a slice of K; lane r of every wave decodes
 // row r, so each wave load of a 16-byte chunk plane reads one contiguous
 // 1 KiB (see the tiled layout in mq_common.h).  The eight waves split the
@@ -121,26 +122,19 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 // oracle/ggml_oracle.c vd_q45_K).  The integer parts are exact, so the result
 // differs from candle's CPU path only in the order of the final f32 adds.
 //
-// Workgroup = R = 64/SL rows of one 64-row weight tile x all of K; wave w
-// takes super-blocks [w*SB, (w+1)*SB) (SB = 1 or 2 dividing K/256, at most
-// 16 waves, so K <= 8192).  Lane (r = lane % R, s = lane / R) handles row r
-// and chunks s*CPL .. s*CPL+CPL-1 (CPL = 8/SL) of each of its super-blocks,
-// so one wave load still reads SL contiguous 16R-byte runs of the tiled
-// layout.  SL is picked so that the 64/R * tiles workgroups spread evenly
-// over the CUs; every output row's sum stays inside its workgroup (added in
-// fixed lane/wave order: deterministic, no cross-workgroup traffic).  All of
-// a wave's loads are issued first (x, scales, then chunks) so that the Q8_K
-// staging waits only for x.
-//
-// Arithmetic per 16-byte qs chunk c of a super-block (32 weights of one row:
-// 16 low nibbles of sub-block 2g and 16 high nibbles of sub-block 2g+1,
-// g = c / 2, elements 64g + 16(c&1) + t and 64g + 32 + 16(c&1) + t):
-// word j's low nibbles (w & 0x0F0F0F0F) are elements 4j..4j+3 of the low run
-// in byte order, the high nibbles ((w >> 4) & 0x0F0F0F0F) those of the high
-// run, so each feeds one v_dot4_i32_i8 against four consecutive Q8_K bytes of
-// x: 3 + 2M VALU ops per 8 weights.
-constexpr int kQ4kMaxWaves = 16;
-constexpr size_t kQ4kMaxLds = 64 * 1024;
+// HBM-bound layout of the work: one 512-thread workgroup per CU owns `rows`
+// consecutive output rows (ceil(n / CUs): 72 at n = 18432, so every CU reads
+// the same number of weight bytes) over all of K.  Thread t takes the
+// (row, super-block) pairs p = t, t + 512, ... (row fastest, so a wave's
+// 16-byte loads of one chunk plane read consecutive rows of the tiled
+// layout), and issues the loads of its first pair before anything else:
+// the weight stream starts at once and the Q8_K staging of x (wave j
+// quantizes super-blocks j, j+8, ... into LDS) runs while it is in flight.
+// Each pair's integer dot reads its 32 Q8_K bytes per 16-byte weight chunk
+// from LDS: 3 + 2M VALU ops per 8 weights.  The pairs' f32 partials go to
+// LDS and thread (row, m) adds them in super-block order (deterministic).
+constexpr int kQ4kThreads = 512;
+constexpr size_t kQ4kMaxLds = 96 * 1024;
 
 // Cross-lane steps through DPP (no LDS round trip).  Lanes a step has no
 // source for (rows outside ROW_MASK) keep their own value.
@@ -168,221 +162,240 @@ __device__ __forceinline__ int sum8(int v) {
   return v;
 }
 
-// LDS bytes of the Q4_K GEMV: Q8_K x (256 quants, d, 8 sub-block sums per
-// super-block and row of x) for all K, and the reduction.
-static size_t q4k_lds_bytes(int64_t nb, int m) {
-  return (size_t)nb * m * (256 + 4 + 32) + (size_t)kQ4kMaxWaves * m * 64 * 4;
+// LDS of the Q4_K GEMV: x as given (f32 or bf16, 256 elements per
+// super-block and row of x), its Q8_K form (256 quants, 8 sub-block sums and
+// d), then one f32 partial per (super-block, row, m).
+__host__ __device__ inline size_t q4k_lds_bytes(int64_t nb, int m, int64_t rows, int xsize) {
+  return (size_t)nb * m * (256 * xsize + 256 + 32 + 4) + (size_t)nb * rows * m * 4;
 }
 
-template <int M, int SB, int SL, typename OUT>
-__global__ __launch_bounds__(kQ4kMaxWaves * 64) void gemv_q4k_kernel(
-    WView w, int64_t n, int64_t nb, const float *__restrict__ x, int64_t ldx, OUT *__restrict__ y, int64_t ldy,
-    const float *__restrict__ bias, int act) {
-  constexpr int R = 64 / SL, CPL = 8 / SL;
-  const int nwaves = blockDim.x >> 6;
+typedef __attribute__((address_space(3))) void lds_void_t;
+// One direct global->LDS load: lane i's 16 bytes from g land at LDS byte
+// address lds + 16 i (M0 carries the LDS address).  Issued as inline asm so
+// that the compiler never holds an in-flight register for x; the kernel
+// orders it with its own s_waitcnt before the barrier that publishes x.
+// s_nop: one wait state between writing M0 and the instruction reading it.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+
+// One (row, super-block) pair's weight bytes.
+struct Q4kPair {
+  uint4 q[8];
+  uint32_t dm, s0, s1, s2;
+};
+
+template <int M, typename XT, typename OUT>
+__global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
+    WView w, int64_t n, int64_t nrows_mem, int nb, int rows, const XT *__restrict__ x, int64_t ldx,
+    OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act) {
   extern __shared__ __align__(16) uint8_t smem[];
-  uint32_t(*xq)[M][64] = reinterpret_cast<uint32_t(*)[M][64]>(smem);                         // [sb][m][dword]
-  int32_t(*xb)[M][8] = reinterpret_cast<int32_t(*)[M][8]>(smem + (size_t)nb * M * 256);    // [sb][m][sub-block]
-  float(*xd)[M] = reinterpret_cast<float(*)[M]>(smem + (size_t)nb * M * 288);              // [sb][m]
-  float(*red)[M][64] = reinterpret_cast<float(*)[M][64]>(smem + (size_t)nb * M * 292);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-  const int64_t tile = blockIdx.x / SL;
-  const int rg = blockIdx.x - (int)(tile * SL);
-  const int r = lane % R, sgrp = lane / R;
-  const int trow = rg * R + r;  // row inside the 64-row tile
-  const int64_t b0 = (int64_t)wave * SB;  // the launcher makes SB divide nb: no partial waves
+  constexpr int kXs = (int)sizeof(XT);
+  const XT *xl = reinterpret_cast<const XT *>(smem);                          // [nb][M][256] x
+  uint8_t *q8 = smem + (size_t)nb * M * 256 * kXs;
+  uint32_t *xq = reinterpret_cast<uint32_t *>(q8);                            // [nb][M][64] packed i8
+  int32_t *xs = reinterpret_cast<int32_t *>(q8 + (size_t)nb * M * 256);       // [nb][M][8]
+  float *xd = reinterpret_cast<float *>(q8 + (size_t)nb * M * 288);           // [nb][M]
+  float *red = reinterpret_cast<float *>(q8 + (size_t)nb * M * 292);          // [nb * rows][M]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int64_t r0 = (int64_t)blockIdx.x * rows;
+  const int npairs = rows * nb;
 
-  // 1. loads, oldest first in the order they are consumed: x (4 floats per
-  //    lane and super-block), the scales, then the qs chunks.
-  float xv[SB][M][4];
+  auto load_pair = [&](int p, Q4kPair &d) {
+    const int sb = p / rows;
+    int64_t row = r0 + (p - sb * rows);
+    row = row < nrows_mem ? row : nrows_mem - 1;  // rows past the padded tiles re-read the last one
+    const int64_t t = row >> 6;
+    const int r = (int)(row & 63);
+    // weights are read once per launch: non-temporal loads keep them from
+    // displacing x and other reused data in L2 / Infinity Cache
+    d.dm = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(bfrag::rec_at(w, 0, 4, t, sb, r)));
+    const uint32_t *sp = reinterpret_cast<const uint32_t *>(bfrag::rec_at(w, 1, 12, t, sb, r));
+    d.s0 = __builtin_nontemporal_load(sp);
+    d.s1 = __builtin_nontemporal_load(sp + 1);
+    d.s2 = __builtin_nontemporal_load(sp + 2);
 #pragma unroll
-  for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const float *xr = x + m * ldx + (b0 + sb) * 256 + 4 * lane;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[sb][m][i] = xr[i];
+    for (int c = 0; c < 8; ++c)
+    {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(bfrag::chunk_at(w, 2, 8, t, sb, c, r)));
+      d.q[c] = make_uint4(v.x, v.y, v.z, v.w);
     }
-  uint4 q[SB][CPL];
-  uint32_t dm[SB], s0[SB], s1[SB], s2[SB];
-#pragma unroll
-  for (int sb = 0; sb < SB; ++sb) {
-    dm[sb] = bfrag::ld4(bfrag::rec_at(w, 0, 4, tile, b0 + sb, trow));
-    const uint8_t *sp = bfrag::rec_at(w, 1, 12, tile, b0 + sb, trow);
-    s0[sb] = bfrag::ld4(sp);
-    s1[sb] = bfrag::ld4(sp + 4);
-    s2[sb] = bfrag::ld4(sp + 8);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // keep this issue order
-#pragma unroll
-  for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-    for (int i = 0; i < CPL; ++i)
-      q[sb][i] = bfrag::ld16(bfrag::chunk_at(w, 2, 8, tile, b0 + sb, sgrp * CPL + i, trow));
+  };
 
-  // 2. Q8_K staging of this wave's super-blocks: lane L holds elements
-  //    4L..4L+3 (sub-block L / 8).
+  // 1. x into LDS by direct loads (item j = sb * M + m is row m's elements
+  //    sb*256 .. +255: one 1 KiB load for f32, half a wave's for bf16), then
+  //    the first two pairs' weights (indices clamped, so every load is
+  //    unconditional).  The explicit wait below leaves the 20 loads issued
+  //    after x's in flight (two pairs: 8 chunk loads, d/dmin and the scale
+  //    record each, none of which can merge), so only x has landed.
+  const int nitems = nb * M;
+  constexpr int kWaves = kQ4kThreads / 64;
+  {
+    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t *)smem;
+    if constexpr (kXs == 4) {
+      for (int j = wave; j < nitems; j += kWaves) {
+        const int sb = j / M, m = j - sb * M;
+        dma16(x + m * ldx + sb * 256 + 4 * lane, lbase + j * 1024);
+      }
+    } else {
+      // two items per load: lanes 0-31 item j, lanes 32-63 item j + 1
+      for (int j = 2 * wave; j < nitems; j += 2 * kWaves) {
+        const int jj = j + (lane >> 5) < nitems ? j + (lane >> 5) : j;
+        const int sb = jj / M, m = jj - sb * M;
+        dma16(x + m * ldx + sb * 256 + 8 * (lane & 31), lbase + j * 512);
+      }
+    }
+  }
+  Q4kPair slot[2];
+  load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
+  load_pair(tid + kQ4kThreads < npairs ? tid + kQ4kThreads : npairs - 1, slot[1]);
+  asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+  __syncthreads();
+
+  // 2. Q8_K staging: lane L holds elements 4L..4L+3 (sub-block L / 8)
+  auto stage = [&](int j) {
+    float v[4];
 #pragma unroll
-  for (int sb = 0; sb < SB; ++sb) {
-    const int64_t bg = b0 + sb;
+    for (int i = 0; i < 4; ++i) v[i] = (float)xl[j * 256 + 4 * lane + i];
+    // largest magnitude over the wave, then the value of its first
+    // occurrence in element order (lowest lane, lowest slot in the lane)
+    const float a0 = __builtin_fabsf(v[0]), a1 = __builtin_fabsf(v[1]);
+    const float a2 = __builtin_fabsf(v[2]), a3 = __builtin_fabsf(v[3]);
+    const float amax = wave_max(__builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3)));
+    const float cand = a0 == amax ? v[0] : a1 == amax ? v[1] : a2 == amax ? v[2] : v[3];
+    const uint64_t hit = __ballot(a0 == amax || a1 == amax || a2 == amax || a3 == amax);
+    const int first = hit ? __builtin_ctzll(hit) : 0;
+    const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), first));
+    uint32_t packed = 0;
+    int qsum = 0;
+    float dx = 0.f;
+    if (amax != 0.f) {
+      const float iscale = -128.f / vmax;
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-      // largest magnitude over the wave, then the value of its first
-      // occurrence in element order (lowest lane, lowest slot in the lane)
-      const float a0 = __builtin_fabsf(xv[sb][m][0]), a1 = __builtin_fabsf(xv[sb][m][1]);
-      const float a2 = __builtin_fabsf(xv[sb][m][2]), a3 = __builtin_fabsf(xv[sb][m][3]);
-      const float amax = wave_max(__builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3)));
-      const float cand = a0 == amax ? xv[sb][m][0]
-                         : a1 == amax ? xv[sb][m][1]
-                         : a2 == amax ? xv[sb][m][2]
-                                      : xv[sb][m][3];
-      const uint64_t hit = __ballot(a0 == amax || a1 == amax || a2 == amax || a3 == amax);
-      const int first = hit ? __builtin_ctzll(hit) : 0;
-      const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), first));
-      uint32_t packed = 0;
-      int qsum = 0;
-      float dx = 0.f;
-      if (amax != 0.f) {
-        const float iscale = -128.f / vmax;
+      for (int i = 0; i < 4; ++i) {
+        const int q = (int)__builtin_fminf(__builtin_roundf(iscale * v[i]), 127.f);
+        qsum += q;
+        packed |= (uint32_t)(q & 0xFF) << (8 * i);
+      }
+      dx = 1.f / iscale;
+    }
+    xq[j * 64 + lane] = packed;
+    qsum = sum8(qsum);
+    if ((lane & 7) == 0) xs[j * 8 + (lane >> 3)] = qsum;
+    if (lane == 0) xd[j] = dx;
+  };
+  for (int j = wave; j < nitems; j += kWaves) stage(j);
+  __syncthreads();
+
+  // 3. per pair: integer dot against Q8_K x, one f32 partial per m
+  auto dot_pair = [&](int p, const Q4kPair &cur) {
+    const bool valid = p < npairs;  // clamped pairs are computed, not stored
+    p = valid ? p : npairs - 1;
+    const int sb = p / rows;
+    // 6-bit scales and mins of sub-blocks 0-3 (low 6 bits of bytes 0-3 / 4-7)
+    // and 4-7 (nibbles of bytes 8-11 with the top 2 bits of bytes 0-3 / 4-7)
+    const uint32_t sc03 = cur.s0 & 0x3F3F3F3Fu, m03 = cur.s1 & 0x3F3F3F3Fu;
+    const uint32_t sc47 = (cur.s2 & 0x0F0F0F0Fu) | ((cur.s0 >> 2) & 0x30303030u);
+    const uint32_t m47 = ((cur.s2 >> 4) & 0x0F0F0F0Fu) | ((cur.s1 >> 2) & 0x30303030u);
+    int sc[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int v = (int)__builtin_fminf(__builtin_roundf(iscale * xv[sb][m][i]), 127.f);
-          qsum += v;
-          packed |= (uint32_t)(v & 0xFF) << (8 * i);
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = (int)((sc03 >> (8 * i)) & 0xFFu);
+      sc[4 + i] = (int)((sc47 >> (8 * i)) & 0xFFu);
+    }
+    int S[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) S[m] = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      // chunks 2g and 2g+1 (32 bytes): low nibbles are elements 64g + 0..31
+      // (sub-block 2g), high nibbles elements 64g + 32..63 (sub-block 2g+1),
+      // each in byte order; one sdot4 chain of 8 per sub-block
+      const uint32_t wd[8] = {cur.q[2 * g].x,     cur.q[2 * g].y,     cur.q[2 * g].z,     cur.q[2 * g].w,
+                              cur.q[2 * g + 1].x, cur.q[2 * g + 1].y, cur.q[2 * g + 1].z, cur.q[2 * g + 1].w};
+      uint32_t lo[8], hi[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        lo[i] = wd[i] & 0x0F0F0F0Fu;
+        hi[i] = (wd[i] >> 4) & 0x0F0F0F0Fu;
+      }
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const uint32_t *xb = xq + (sb * M + m) * 64 + 16 * g;
+        const uint4 x0 = *reinterpret_cast<const uint4 *>(xb);
+        const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 4);
+        const uint4 x2 = *reinterpret_cast<const uint4 *>(xb + 8);
+        const uint4 x3 = *reinterpret_cast<const uint4 *>(xb + 12);
+        const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          dl = __builtin_amdgcn_sdot4((int)lo[i], (int)xl[i], dl, false);
+          dh = __builtin_amdgcn_sdot4((int)hi[i], (int)xh[i], dh, false);
         }
-        dx = 1.f / iscale;
+        // |dl|, |dh| <= 32 * 15 * 128 < 2^16: the 24-bit products are exact
+        S[m] += __mul24(sc[2 * g], dl) + __mul24(sc[2 * g + 1], dh);
       }
-      xq[bg][m][lane] = packed;
-      qsum = sum8(qsum);
-      if ((lane & 7) == 0) xb[bg][m][lane >> 3] = qsum;
-      if (lane == 0) xd[bg][m] = dx;
     }
-  }
-  __syncthreads();
-
-  // 3. integer dot products, consumed in two halves of the chunk loads, each
-  //    behind its own wait, so the first half's arithmetic overlaps the
-  //    second half's loads.
-  int32_t S[SB][M];
-#pragma unroll
-  for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-    for (int m = 0; m < M; ++m) S[sb][m] = 0;
-  constexpr int kLoads = SB * CPL, kFirst = kLoads / 2;  // chunks in the first half (may be 0)
-  static_for<2>([&]<int HALF>() {
-    constexpr int after = HALF == 0 ? kLoads - kFirst : 0;  // chunk loads issued after this half
-    constexpr int count = HALF == 0 ? kFirst : kLoads - kFirst;
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt((after & 15) | ((after >> 4) << 14) | (0xF << 8) | (7 << 4));
-    static_for<count>([&]<int LI>() {
-      constexpr int li = (HALF == 0 ? 0 : kFirst) + LI;
-      constexpr int sb = li / CPL, i = li % CPL;
-      const int c = sgrp * CPL + i;  // compile-time when SL == 1
-      const int g = c >> 1, hs = c & 1;
-      // sub-blocks 2g (low nibbles) and 2g+1 (high): bytes (2g)&3, (2g+1)&3 of
-      // the packed 6-bit scale words for sub-blocks 0-3 (g < 2) or 4-7
-      const uint32_t scw = g < 2 ? (s0[sb] & 0x3F3F3F3Fu) : ((s2[sb] & 0x0F0F0F0Fu) | ((s0[sb] >> 2) & 0x30303030u));
-      const int sh = 16 * (g & 1);
-      const int sclo = (int)((scw >> sh) & 0xFFu), schi = (int)((scw >> (sh + 8)) & 0xFFu);
-      const uint32_t wd[4] = {q[sb][i].x, q[sb][i].y, q[sb][i].z, q[sb][i].w};
-      uint32_t lo[4], hi[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        lo[j] = wd[j] & 0x0F0F0F0Fu;
-        hi[j] = (wd[j] >> 4) & 0x0F0F0F0Fu;
-      }
-      const int64_t bg = b0 + sb;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const uint4 xa = *reinterpret_cast<const uint4 *>(&xq[bg][m][16 * g + 4 * hs]);
-        const uint4 xc = *reinterpret_cast<const uint4 *>(&xq[bg][m][16 * g + 8 + 4 * hs]);
-        int il = __builtin_amdgcn_sdot4((int)lo[0], (int)xa.x, 0, false);
-        il = __builtin_amdgcn_sdot4((int)lo[1], (int)xa.y, il, false);
-        il = __builtin_amdgcn_sdot4((int)lo[2], (int)xa.z, il, false);
-        il = __builtin_amdgcn_sdot4((int)lo[3], (int)xa.w, il, false);
-        int ih = __builtin_amdgcn_sdot4((int)hi[0], (int)xc.x, 0, false);
-        ih = __builtin_amdgcn_sdot4((int)hi[1], (int)xc.y, ih, false);
-        ih = __builtin_amdgcn_sdot4((int)hi[2], (int)xc.z, ih, false);
-        ih = __builtin_amdgcn_sdot4((int)hi[3], (int)xc.w, ih, false);
-        S[sb][m] += __mul24(sclo, il) + __mul24(schi, ih);  // |il|, |ih| < 2^15: 24-bit products are exact
-      }
-    });
-  });
-
-  // 4. per super-block f32 combine: (d_w d_x) S - (dmin_w d_x) sum_s m_s B_s,
-  //    the mins term once per row (lane group 0)
-  float acc[M];
-#pragma unroll
-  for (int m = 0; m < M; ++m) acc[m] = 0.f;
-#pragma unroll
-  for (int sb = 0; sb < SB; ++sb) {
-    const int64_t bg = b0 + sb;
-    const float d = h2f((uint16_t)(dm[sb] & 0xFFFF)), dmin = h2f((uint16_t)(dm[sb] >> 16));
-    const uint32_t mlo = s1[sb] & 0x3F3F3F3Fu;
-    const uint32_t mhi = ((s2[sb] >> 4) & 0x0F0F0F0Fu) | ((s1[sb] >> 2) & 0x30303030u);
+    const float d = h2f((uint16_t)(cur.dm & 0xFFFF)), dmin = h2f((uint16_t)(cur.dm >> 16));
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const float dx = xd[bg][m];
-      int smin = 0;
-      if (sgrp == 0) {
-        const int4 ba = *reinterpret_cast<const int4 *>(&xb[bg][m][0]);
-        const int4 bb = *reinterpret_cast<const int4 *>(&xb[bg][m][4]);
-        smin = __mul24((int)(mlo & 0xFF), ba.x) + __mul24((int)((mlo >> 8) & 0xFF), ba.y) +
-               __mul24((int)((mlo >> 16) & 0xFF), ba.z) + __mul24((int)(mlo >> 24), ba.w) +
-               __mul24((int)(mhi & 0xFF), bb.x) + __mul24((int)((mhi >> 8) & 0xFF), bb.y) +
-               __mul24((int)((mhi >> 16) & 0xFF), bb.z) + __mul24((int)(mhi >> 24), bb.w);
-      }
-      acc[m] = __builtin_fmaf(d * dx, (float)S[sb][m], acc[m]);
-      acc[m] = __builtin_fmaf(-(dmin * dx), (float)smin, acc[m]);
+      const int j = sb * M + m;
+      const int4 ba = *reinterpret_cast<const int4 *>(xs + j * 8);
+      const int4 bb = *reinterpret_cast<const int4 *>(xs + j * 8 + 4);
+      const int smin = __mul24((int)(m03 & 0xFF), ba.x) + __mul24((int)((m03 >> 8) & 0xFF), ba.y) +
+                       __mul24((int)((m03 >> 16) & 0xFF), ba.z) + __mul24((int)(m03 >> 24), ba.w) +
+                       __mul24((int)(m47 & 0xFF), bb.x) + __mul24((int)((m47 >> 8) & 0xFF), bb.y) +
+                       __mul24((int)((m47 >> 16) & 0xFF), bb.z) + __mul24((int)(m47 >> 24), bb.w);
+      const float dx = xd[j];
+      if (valid) red[p * M + m] = __builtin_fmaf(d * dx, (float)S[m], -(dmin * dx) * (float)smin);
     }
+  };
+  // the two preloaded pairs run straight-line (so each waits only for its
+  // own loads); pairs past them (K beyond 2 * 512 pairs) load as they go
+  dot_pair(tid, slot[0]);
+  dot_pair(tid + kQ4kThreads, slot[1]);
+  for (int p = tid + 2 * kQ4kThreads; p < npairs; p += kQ4kThreads) {
+    load_pair(p, slot[0]);
+    dot_pair(p, slot[0]);
   }
-
-  // 5. add the partial sums in lane-group, then wave order
-#pragma unroll
-  for (int m = 0; m < M; ++m) red[wave][m][lane] = acc[m];
   __syncthreads();
-  if (wave == 0 && lane < R) {
-    const int64_t row = tile * kRowTile + rg * R + lane;
-    if (row < n) {
-      const float bv = bias ? bias[row] : 0.f;
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        float t = 0.f;
-        for (int wv = 0; wv < nwaves; ++wv)
-#pragma unroll
-          for (int sg = 0; sg < SL; ++sg) t += red[wv][m][sg * R + lane];
-        store1<OUT>(y + m * ldy + row, apply_act(t + bv, act));
-      }
-    }
+
+  // 4. thread (row, m) adds its row's partials in super-block order
+  for (int t = tid; t < rows * M; t += kQ4kThreads) {
+    const int m = t / rows, rl = t - m * rows;
+    const int64_t row = r0 + rl;
+    if (row >= n) continue;
+    float acc = 0.f;
+    for (int sb = 0; sb < nb; ++sb) acc += red[(sb * rows + rl) * M + m];
+    if (bias) acc += bias[row];
+    store1<OUT>(y + m * ldy + row, apply_act(acc, act));
   }
 }
 
-// Super-blocks per wave for the Q4_K path (0: use the generic kernel).
-static int q4k_sb(int64_t nb, int64_t m) {
-  if (q4k_lds_bytes(nb, (int)m) > kQ4kMaxLds) return 0;
-  if (nb <= kQ4kMaxWaves) return 1;
-  // two super-blocks per wave fit 128 VGPRs up to m = 4; SB must divide nb
-  if (nb <= 2 * kQ4kMaxWaves && nb % 2 == 0 && m <= 4) return 2;
-  return 0;
+// Rows per workgroup of the Q4_K path (0: use the generic kernel): one
+// workgroup per CU, fewer rows when the LDS would not hold them.
+static int q4k_rows(int64_t n, int64_t nb, int64_t m, int cus) {
+  int64_t rows = (n + cus - 1) / cus;
+  if (rows < 1) rows = 1;
+  while (rows > 8 && q4k_lds_bytes(nb, (int)m, rows, 4) > kQ4kMaxLds) rows = (rows + 1) / 2;
+  if (q4k_lds_bytes(nb, (int)m, rows, 4) > kQ4kMaxLds) return 0;
+  return (int)rows;
 }
 
-// Lane groups per row (rows per workgroup = 64 / SL): the split that spreads
-// ntiles * SL workgroups most evenly over the CUs while every wave of the
-// launch is resident at once (at most 16 waves per CU: a second round would
-// pay the memory latency again); fewest workgroups on a tie.
-static int q4k_sl(int64_t ntiles, int64_t waves_per_wg, int cus) {
-  double best = -1.0;
-  int pick = 1;
-  for (int sl : {1, 2, 4, 8}) {
-    const int64_t wgs = ntiles * sl;
-    if (sl > 1 && wgs * waves_per_wg > (int64_t)cus * 16) break;
-    const double eff = (double)wgs / (double)(((wgs + cus - 1) / cus) * cus);
-    if (eff > best + 1e-9) {
-      best = eff;
-      pick = sl;
-    }
-  }
-  return pick;
+template <int M, typename XT, typename OUT>
+static void launch_gemv_q4k(const WView &w, int64_t n, int64_t k, const XT *x, int64_t ldx, OUT *y, int64_t ldy,
+                            const float *bias, int act, int cus, hipStream_t stream) {
+  const int64_t nb = k / 256;
+  const int rows = q4k_rows(n, nb, M, cus);
+  const int64_t wgs = (n + rows - 1) / rows;
+  const int64_t nrows_mem = ((n + kRowTile - 1) / kRowTile) * kRowTile;
+  hipLaunchKernelGGL((gemv_q4k_kernel<M, XT, OUT>), dim3((unsigned)wgs), dim3(kQ4kThreads),
+                     q4k_lds_bytes(nb, M, rows, (int)sizeof(XT)), stream, w, n, nrows_mem, (int)nb, rows, x, ldx, y,
+                     ldy, bias, act);
 }
 
 static int pick_ksplit(int64_t ntiles, int64_t k) {
@@ -393,42 +406,12 @@ static int pick_ksplit(int64_t ntiles, int64_t k) {
   return (int)ks;
 }
 
-size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k) {
-  if (type == Q4_K && q4k_sb(k / 256, m)) return 0;
+size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k, int cus) {
+  if (type == Q4_K && q4k_rows(n, k / 256, m, cus)) return 0;
   const int64_t ntiles = (n + kRowTile - 1) / kRowTile;
   const int ks = pick_ksplit(ntiles, k);
   if (ks == 1) return 0;
   return (size_t)ks * m * ntiles * kRowTile * sizeof(float);
-}
-
-template <int M, int SB, int SL, typename OUT>
-static void launch_gemv_q4k_sl(const WView &w, int64_t n, int64_t nb, const float *x, int64_t ldx, OUT *y,
-                               int64_t ldy, const float *bias, int act, hipStream_t stream) {
-  const int64_t ntiles = (n + kRowTile - 1) / kRowTile;
-  const int waves = (int)(nb / SB);
-  hipLaunchKernelGGL((gemv_q4k_kernel<M, SB, SL, OUT>), dim3((unsigned)(ntiles * SL)), dim3(waves * 64),
-                     q4k_lds_bytes(nb, M), stream, w, n, nb, x, ldx, y, ldy, bias, act);
-}
-
-template <int M, int SB, typename OUT>
-static void launch_gemv_q4k_sb(const WView &w, int64_t n, int64_t nb, const float *x, int64_t ldx, OUT *y,
-                               int64_t ldy, const float *bias, int act, int cus, hipStream_t stream) {
-  switch (q4k_sl((n + kRowTile - 1) / kRowTile, nb / SB, cus)) {
-    case 1: launch_gemv_q4k_sl<M, SB, 1, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, stream); break;
-    case 2: launch_gemv_q4k_sl<M, SB, 2, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, stream); break;
-    case 4: launch_gemv_q4k_sl<M, SB, 4, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, stream); break;
-    default: launch_gemv_q4k_sl<M, SB, 8, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, stream); break;
-  }
-}
-
-template <int M, typename OUT>
-static void launch_gemv_q4k(const WView &w, int64_t n, int64_t k, const float *x, int64_t ldx, OUT *y, int64_t ldy,
-                            const float *bias, int act, int cus, hipStream_t stream) {
-  const int64_t nb = k / 256;
-  if (q4k_sb(nb, M) == 1)
-    launch_gemv_q4k_sb<M, 1, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, cus, stream);
-  else if constexpr (M <= 4)
-    launch_gemv_q4k_sb<M, 2, OUT>(w, n, nb, x, ldx, y, ldy, bias, act, cus, stream);
 }
 
 template <int TYPE, int M, typename OUT>
@@ -446,22 +429,24 @@ static void launch_gemv_t(const WView &w, int64_t n, int64_t k, const float *x, 
   }
 }
 
+template <typename XT, typename OUT>
+static void launch_gemv_q4k_m(const WView &w, int64_t n, int64_t k, const XT *x, int64_t m, int64_t ldx, OUT *y,
+                              int64_t ldy, const float *bias, int act, int cus, hipStream_t stream) {
+  switch (m) {
+    case 1: launch_gemv_q4k<1, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 2: launch_gemv_q4k<2, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 3: launch_gemv_q4k<3, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 4: launch_gemv_q4k<4, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 5: launch_gemv_q4k<5, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 6: launch_gemv_q4k<6, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    case 7: launch_gemv_q4k<7, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+    default: launch_gemv_q4k<8, XT, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
+  }
+}
+
 template <int TYPE, typename OUT>
 static void launch_gemv_m(const WView &w, int64_t n, int64_t k, const float *x, int64_t m, int64_t ldx,
-                          OUT *y, int64_t ldy, const float *bias, int act, float *partial, int cus,
-                          hipStream_t stream) {
-  if (TYPE == Q4_K && q4k_sb(k / 256, m)) {
-    switch (m) {
-      case 1: launch_gemv_q4k<1, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 2: launch_gemv_q4k<2, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 3: launch_gemv_q4k<3, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 4: launch_gemv_q4k<4, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 5: launch_gemv_q4k<5, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 6: launch_gemv_q4k<6, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      case 7: launch_gemv_q4k<7, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-      default: launch_gemv_q4k<8, OUT>(w, n, k, x, ldx, y, ldy, bias, act, cus, stream); return;
-    }
-  }
+                          OUT *y, int64_t ldy, const float *bias, int act, float *partial, hipStream_t stream) {
   switch (m) {
     case 1: launch_gemv_t<TYPE, 1, OUT>(w, n, k, x, ldx, y, ldy, bias, act, partial, stream); break;
     case 2: launch_gemv_t<TYPE, 2, OUT>(w, n, k, x, ldx, y, ldy, bias, act, partial, stream); break;
@@ -474,17 +459,47 @@ static void launch_gemv_m(const WView &w, int64_t n, int64_t k, const float *x, 
   }
 }
 
-hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const float *x, int64_t m,
+// The Q4_K kernel's direct x loads need 16-byte aligned rows of x.
+static bool q4k_x_aligned(const void *x, int x_type, int64_t ldx) {
+  const int64_t es = x_type == F32 ? 4 : 2;
+  return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ldx * es) % 16 == 0;
+}
+
+bool gemv_reads_x_in_place(int type, int64_t m, int64_t n, int64_t k, const void *x, int x_type, int64_t ldx,
+                           int cus) {
+  return type == Q4_K && m >= 1 && m <= kGemvMaxM && q4k_rows(n, k / 256, m, cus) > 0 &&
+         q4k_x_aligned(x, x_type, ldx);
+}
+
+hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const void *x, int x_type, int64_t m,
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
                        float *partial, int cus, hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
+  if (gemv_reads_x_in_place(type, m, n, k, x, x_type, ldx, cus)) {
+    if (x_type == F32) {
+      if (y_type == F32)
+        launch_gemv_q4k_m<float, float>(w, n, k, static_cast<const float *>(x), m, ldx, static_cast<float *>(y),
+                                        ldy, bias, act, cus, stream);
+      else
+        launch_gemv_q4k_m<float, __bf16>(w, n, k, static_cast<const float *>(x), m, ldx,
+                                         static_cast<__bf16 *>(y), ldy, bias, act, cus, stream);
+    } else {
+      if (y_type == F32)
+        launch_gemv_q4k_m<__bf16, float>(w, n, k, static_cast<const __bf16 *>(x), m, ldx,
+                                         static_cast<float *>(y), ldy, bias, act, cus, stream);
+      else
+        launch_gemv_q4k_m<__bf16, __bf16>(w, n, k, static_cast<const __bf16 *>(x), m, ldx,
+                                          static_cast<__bf16 *>(y), ldy, bias, act, cus, stream);
+    }
+    return hipGetLastError();
+  }
+  if (x_type != F32) return hipErrorInvalidValue;  // the generic kernel reads f32 x
+  const float *xf = static_cast<const float *>(x);
   bool ok = dispatch_type(type, [&]<int T>() {
     if (y_type == F32)
-      launch_gemv_m<T, float>(w, n, k, x, m, ldx, static_cast<float *>(y), ldy, bias, act, partial, cus,
-                              stream);
+      launch_gemv_m<T, float>(w, n, k, xf, m, ldx, static_cast<float *>(y), ldy, bias, act, partial, stream);
     else
-      launch_gemv_m<T, __bf16>(w, n, k, x, m, ldx, static_cast<__bf16 *>(y), ldy, bias, act, partial, cus,
-                               stream);
+      launch_gemv_m<T, __bf16>(w, n, k, xf, m, ldx, static_cast<__bf16 *>(y), ldy, bias, act, partial, stream);
   });
   if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();

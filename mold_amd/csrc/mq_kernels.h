@@ -23,13 +23,17 @@ hipError_t launch_widen_bf16(const __bf16 *x, int64_t m, int64_t k, int64_t ldx,
 hipError_t launch_stage_bf16(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, __bf16 *out,
                              int64_t kp, hipStream_t stream);
 
-// Skinny-M GEMV (m <= kGemvMaxM).  `partial` is scratch of
-// ksplit*m*ntiles*64 floats when the launcher decides to split K across
-// workgroups (gemv_scratch_bytes returns what it needs; 0 for the Q4_K path,
-// which adds its K-split partials inside the workgroup).
+// Skinny-M GEMV (m <= kGemvMaxM).  Q4_K weights (the modulation linears)
+// take a kernel that reads f32 or bf16 x with 16-byte aligned rows in place
+// and needs no scratch (gemv_reads_x_in_place); everything else reads f32 x
+// (contiguous f32 x of the Q4_K shapes also takes the Q4_K kernel) and the
+// generic kernel, when it splits K across workgroups, uses `partial` scratch
+// of gemv_scratch_bytes.
 constexpr int kGemvMaxM = 8;
-size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k);
-hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const float *x, int64_t m,
+bool gemv_reads_x_in_place(int type, int64_t m, int64_t n, int64_t k, const void *x, int x_type, int64_t ldx,
+                           int cus);
+size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k, int cus);
+hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const void *x, int x_type, int64_t m,
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
                        float *partial, int cus, hipStream_t stream);
 
