@@ -29,27 +29,54 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 GEMM_TOL = 1e-2   # BASELINE: rel-L2 <= 1e-2 vs f32 dequantize-then-matmul
-GEMV_TOL = 1e-5   # same products as the reference algorithm; only f32 summation order differs
+GEMV_TOL = 1e-5   # exact weights (or exact Q8_K products) summed in f32
+
+
+def _q8k_row_bound(x, blocks, t, n, k):
+    """Per-output bound on |y_gpu - y_exact| for a GEMV that quantizes x to Q8_K.
+
+    Whatever Q8_K's rounding convention (scale -128/max or -127/max, ties to even or
+    away from zero, the +max clamp to 127), every quantized element is within one
+    step d_x = max|x_sb| / 127 of x, so |sum_i w_i (x_i - q_i d_x)| <= sum_sb d_x
+    sum_{i in sb} |w_i|.  The f32 combine adds at most ~K ulps of sum |w x|.  The bound
+    therefore holds for any correct Q8_K GEMV and fails on a wrong scale, a dropped
+    term or a misplaced super-block (errors of order |y|)."""
+    w = O.dequantize(t, blocks, n, k).astype(np.float64)
+    xa = np.abs(x.astype(np.float64)).reshape(x.shape[0], k // 256, 256)
+    dx = xa.max(axis=2) / 127.0                                   # [m, sb]
+    wa = np.abs(w).reshape(n, k // 256, 256).sum(axis=2)           # [n, sb]
+    quant = dx @ wa.T                                              # [m, n]
+    f32 = 4 * k * 2.0 ** -24 * (np.abs(x.astype(np.float64)) @ np.abs(w).T)
+    return quant + f32 + 1e-30
 
 
 def _gemv_check(t, x, y, blocks, n, k, extra=None):
-    """GEMV parity.  The Q4_K fast path runs candle's k-quant algorithm (x quantized to
-    Q8_K, integer block dots, one f32 combine per super-block), so it is held to GEMV_TOL
-    against the oracle's restatement of candle's CPU QMatMul on the same blocks; the
-    generic path (other types, and Q4_K with k > 8192) accumulates exact weights times f32
-    x in f32 and is held to GEMV_TOL against the f64 dequantize-then-matmul.  Both also
-    meet the BASELINE 1e-2 bar against the exact f32 activations."""
+    """GEMV parity on pinned references only.
+
+    * Every type: rel-L2 <= 1e-2 against the f64 dequantize-then-matmul (the BASELINE
+      bar) and finite outputs.
+    * Q4_K (the kernel quantizes x to Q8_K, candle's k-quant algorithm): every output
+      within _q8k_row_bound of the exact product.
+    * Other types (exact weights times f32 x, summed in f32): rel-L2 <= 1e-5 against f64.
+    Agreement with the oracle's restatement of candle's CPU QMatMul is printed, not
+    asserted: that restatement's Q8_K conventions come from candle's source, which is
+    not in this container (parity unpinned)."""
     ref_exact = O.matmul_f64(int(t), x, blocks, n, k)
-    refs = [ref_exact]
-    if int(t) == O.Q4_K:
-        refs.append(O.matmul_candle(int(t), x, blocks, n, k).astype(np.float64))
     if extra is not None:
         ref_exact = extra(ref_exact)
-        refs = [extra(r) for r in refs]
-    err = min(O.rel_l2(y, r) for r in refs)
-    assert err <= GEMV_TOL, err
-    assert O.rel_l2(y, ref_exact) <= GEMM_TOL
     assert np.isfinite(y).all()
+    assert O.rel_l2(y, ref_exact) <= GEMM_TOL
+    if int(t) == O.Q4_K:
+        if extra is None:
+            bound = _q8k_row_bound(x, blocks, int(t), n, k)
+            err = np.abs(y.astype(np.float64) - ref_exact)
+            assert (err <= bound).all(), float((err / bound).max())
+        cand = O.matmul_candle(int(t), x, blocks, n, k).astype(np.float64)
+        if extra is not None:
+            cand = extra(cand)
+        print(f"[report] Q4_K GEMV vs candle CPU restatement: rel-L2 {O.rel_l2(y, cand):.2e}", flush=True)
+    else:
+        assert O.rel_l2(y, ref_exact) <= GEMV_TOL
 
 
 def _say(msg):
@@ -193,15 +220,16 @@ def test_gemv_bias_gelu_strides_bf16(dev, torch):
 
 
 def test_gemv_q8k_activation_edge_cases(dev, torch):
-    """Q8_K staging of the Q4_K GEMV: the scale comes from the first element of largest
-    magnitude (ties in |x| with opposite signs, -max and +max), all-zero super-blocks give
-    d = 0, a lone non-zero element quantizes to -128, and values at +-max clamp to 127."""
+    """Q8_K staging of the Q4_K GEMV on awkward activations: ties in |x| with opposite
+    signs, all-zero super-blocks (d = 0), a lone non-zero element, a constant block (every
+    q at the clamp), a tiny scale.  Each row must stay inside the convention-independent
+    Q8_K error bound of the exact product, and rows of zeros must give exact zeros."""
     t, n, k = GgmlDType.Q4_K, 128, 1024
     _say("gemv Q8_K activation edge cases")
     blocks = _weights(int(t), n, k, seed=77)
     qt = QTensor.from_blocks(dev, t, (n, k), blocks)
     rng = np.random.default_rng(78)
-    x = rng.standard_normal((4, k)).astype(np.float32)
+    x = rng.standard_normal((5, k)).astype(np.float32)
     x[0, 3], x[0, 200] = -2.5, 2.5           # tie: element 3 (negative) comes first
     x[0, 300], x[0, 301] = 3.0, -3.0         # second super-block: + first
     x[1, :256] = 0.0                         # zero super-block
@@ -209,12 +237,39 @@ def test_gemv_q8k_activation_edge_cases(dev, torch):
     x[1, 400] = 1.5                          # lone element
     x[2, 512:768] = 1.0                      # constant block: every q = -128
     x[3, 768:] *= 1e-30                      # tiny scale
+    x[4] = 0.0                               # all zero
     y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
-    cand = O.matmul_candle(int(t), x, blocks, n, k)
     assert np.isfinite(y).all()
-    assert O.rel_l2(y, cand) <= GEMV_TOL
-    for r in range(4):
-        assert O.rel_l2(y[r], cand[r]) <= GEMV_TOL, r
+    assert not y[4].any()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    err = np.abs(y.astype(np.float64) - ref)
+    assert (err <= _q8k_row_bound(x, blocks, int(t), n, k)).all()
+    cand = O.matmul_candle(int(t), x, blocks, n, k)
+    print(f"[report] edge cases vs candle CPU restatement: rel-L2 {O.rel_l2(y, cand):.2e}", flush=True)
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_gemv_q4k_exact_on_q8k_grid(dev, torch, m):
+    """Activations already on a Q8_K grid: per super-block x = c * q with integer q in
+    [-127, 127] and one element at -128 c (the unique element of largest magnitude, so the
+    scale -128 / max reproduces c exactly and every q is representable).  Quantization is
+    then lossless, so the GEMV's integer dots and its d_w * d_x, dmin_w * d_x combine must
+    equal the exact product up to f32 summation (1e-5).  A wrong activation scale (e.g.
+    -127 / max), a wrong sub-block sum or a misplaced nibble fails this by orders of
+    magnitude; the rounding tie rule is not exercised (no ties)."""
+    t, n, k = GgmlDType.Q4_K, 448, 2048
+    _say(f"gemv Q4_K exact on the Q8_K grid m={m}")
+    blocks = _weights(int(t), n, k, seed=90 + m)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    rng = np.random.default_rng(91 + m)
+    q = rng.integers(-127, 128, size=(m, k // 256, 256))
+    q[:, :, 17] = -128
+    c = np.ldexp(1.0, rng.integers(-12, -4, size=(m, k // 256, 1)))   # powers of two: c * q exact in f32
+    x = (q * c).reshape(m, k).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    assert np.isfinite(y).all()
+    assert O.rel_l2(y, ref) <= GEMV_TOL, O.rel_l2(y, ref)
 
 
 @pytest.mark.parametrize("n,k,m", [(64 * 37, 3072, 1), (64 * 37, 3072, 3), (320, 4096, 2), (200, 2048, 8)])
@@ -351,9 +406,10 @@ def test_gemm_and_gemv_deterministic(dev, torch):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), m
 
 
-def test_gpu_within_bar_of_candle_cpu_algorithm(dev, torch):
-    # candle's CPU QMatMul quantizes x to Q8_0/Q8_1/Q8_K first; both it and the
-    # GPU path must sit inside the 1e-2 envelope of the exact reference.
+def test_gpu_and_candle_cpu_algorithm_within_bar(dev, torch):
+    """candle's CPU QMatMul quantizes x to Q8_0/Q8_1/Q8_K first.  Both the GPU path and the
+    oracle's restatement of candle's CPU algorithm must sit inside the 1e-2 envelope of the
+    exact f64 product (the pinned bar); their mutual distance is reported."""
     _say("gpu vs candle cpu algorithm")
     m, n, k = 64, 256, 1024
     x = np.random.default_rng(41).standard_normal((m, k)).astype(np.float32)
@@ -361,9 +417,11 @@ def test_gpu_within_bar_of_candle_cpu_algorithm(dev, torch):
         blocks = _weights(int(t), n, k, seed=42)
         qt = QTensor.from_blocks(dev, t, (n, k), blocks)
         y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+        exact = O.matmul_f64(int(t), x, blocks, n, k)
         cand = O.matmul_candle(int(t), x, blocks, n, k)
-        assert O.rel_l2(y, cand) <= 2 * GEMM_TOL, t.name
-        assert O.rel_l2(cand, O.matmul_f64(int(t), x, blocks, n, k)) <= GEMM_TOL, t.name
+        assert O.rel_l2(y, exact) <= GEMM_TOL, t.name
+        assert O.rel_l2(cand, exact) <= GEMM_TOL, t.name
+        print(f"[report] {t.name}: GPU vs candle CPU restatement rel-L2 {O.rel_l2(y, cand):.2e}", flush=True)
 
 
 # --------------------------------------------------------- errors and edges
