@@ -16,8 +16,12 @@
  *   - Work is enqueued on `stream` (a hipStream_t; NULL is the null stream)
  *     and is asynchronous unless stated otherwise.
  *   - A context is bound to one device; call it from one thread at a time.
- *     Its scratch buffer is shared by every call on that context, so calls
- *     that use scratch must be ordered on one stream.
+ *     Scratch memory (activation staging, split-K partial sums) is kept per
+ *     stream, so quantized matmuls on different streams of one context may
+ *     run concurrently.  A stream's workspace only grows, and an outgrown
+ *     one is released with the context, so no mq_qmatmul call synchronizes
+ *     or frees device memory; it allocates only when its stream's workspace
+ *     is too small (mq_ctx_reserve_stream_scratch pre-sizes it).
  */
 #ifndef MOLDQ_H
 #define MOLDQ_H
@@ -70,15 +74,29 @@ void mq_ctx_destroy(mq_ctx *ctx);
 /* Pre-allocate one HBM arena that later uploads are carved from (bump
  * allocation, released with the context).  Optional. */
 int mq_ctx_reserve_arena(mq_ctx *ctx, size_t bytes);
-/* Pre-size the scratch buffer used for f32->bf16 activation staging so that
- * mq_qmatmul never allocates.  Optional. */
+/* Minimum size of every stream workspace (activation staging and split-K
+ * partials): grows the workspaces of the streams seen so far and of the null
+ * stream to `bytes` now, and later streams' on their first call.  Optional. */
 int mq_ctx_reserve_scratch(mq_ctx *ctx, size_t bytes);
+/* Grow the workspace of one stream (a hipStream_t) to at least `bytes` now,
+ * e.g. before capturing that stream into a HIP graph: a call that would
+ * have to grow the workspace of a stream under capture fails with
+ * MQ_E_INVALID instead.  Optional. */
+int mq_ctx_reserve_stream_scratch(mq_ctx *ctx, void *stream, size_t bytes);
+/* Workspace bytes a quantized matmul of `m` rows against w needs (gated != 0
+ * for mq_qmatmul_gated_add), the maximum over every x placement and stride:
+ * the size to reserve before capturing such calls into a graph.  No
+ * counterpart in candle, whose CUDA matmuls allocate per call. */
+int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int64_t m, int gated,
+                              size_t *bytes);
 
 /* Upload a GGUF weight (blocks exactly as stored in the file) to the device.
  * Replaces QCudaStorage load_quantized / `content.tensor(reader, name, device)`
  * (crates/mold-inference/src/flux/lora.rs:722) and VarBuilder::from_gguf
  * (crates/mold-inference/src/flux/pipeline.rs:976).  Synchronous: the host
- * buffer may be reused on return.  nbytes must equal n*k/bs*type_size. */
+ * buffer may be reused on return.  nbytes must equal n*k/bs*type_size.
+ * The raw blocks pass through a context-owned device staging buffer that
+ * grows to the largest tensor uploaded and is kept. */
 int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
                       const void *host_blocks, size_t nbytes, mq_qtensor **out);
 /* Same from GGUF blocks already in device memory (copied; caller keeps its
@@ -93,7 +111,7 @@ int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
  * QTensor::quantize / quantize_onto (crates/mold-inference/src/flux/
  * pipeline.rs:219-229, crates/mold-inference/src/flux/lora.rs:849).
  * Runs on `stream` after work already queued there and returns when the
- * blocks are in place (it uses and frees a temporary staging buffer). */
+ * blocks are in place (through the context's upload staging buffer). */
 int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld,
                 void *stream, mq_qtensor **out);
 /* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
@@ -177,7 +195,9 @@ int64_t mq_gguf_find(const mq_gguf *g, const char *name);
 int mq_gguf_tensor_info(const mq_gguf *g, int64_t index, const char **name, int *dtype,
                         int *n_dims, int64_t dims[4], uint64_t *file_offset, size_t *nbytes);
 /* Read a 2-D quantized tensor from the file and upload it (content.tensor(
- * reader, name, device)). */
+ * reader, name, device)): the file is read in 16 MiB chunks into two pinned
+ * host buffers in turn, each copied to the device asynchronously while the
+ * next is read, then repacked on the device.  Synchronous. */
 int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out);
 
 #ifdef __cplusplus

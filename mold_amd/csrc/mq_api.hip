@@ -3,11 +3,15 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <unistd.h>
 
+#include <algorithm>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/moldq.h"
+#include "mq_internal.h"
 #include "mq_kernels.h"
 
 using namespace mq;
@@ -19,19 +23,25 @@ struct mq_ctx {
   uint8_t *arena = nullptr;
   size_t arena_size = 0;
   size_t arena_used = 0;
-  // Scratch: activation staging and GEMV partial sums.
-  void *scratch = nullptr;
-  size_t scratch_size = 0;
-  // GEMM tail-tile partial sums, one buffer per stream (so GEMMs with
-  // in-place bf16 x may run concurrently on different streams).
-  struct StreamBuf {
+  // Per-stream workspaces: f32 -> bf16 activation staging, GEMM tail partial
+  // sums, generic-GEMV partials and widened x.  A stream's workspace only
+  // grows: the outgrown buffer is kept (retired) until the context is
+  // destroyed, so no call synchronizes or frees, and work already queued (or
+  // captured in a graph) never sees its buffer released.
+  struct Ws {
     hipStream_t stream = nullptr;
-    void *p = nullptr;
+    uint8_t *p = nullptr;
     size_t size = 0;
   };
-  static constexpr int kTailStreams = 4;
-  StreamBuf tail[kTailStreams];
-  int tail_used = 0;
+  std::vector<Ws> ws;
+  std::vector<void *> retired;
+  size_t ws_floor = 0;  // mq_ctx_reserve_scratch: minimum size of every workspace
+  // Upload staging: a device buffer for raw GGUF blocks (grows, kept) and two
+  // pinned host buffers for file reads (allocated on the first GGUF load).
+  uint8_t *dstage = nullptr;
+  size_t dstage_size = 0;
+  uint8_t *pinned[2] = {nullptr, nullptr};
+  hipStream_t upload_stream = nullptr;
 };
 
 struct mq_qtensor {
@@ -83,6 +93,10 @@ struct DeviceGuard {
   }
 };
 
+constexpr size_t kMiB = size_t(1) << 20;
+size_t round_mib(size_t b) { return (b + kMiB - 1) & ~(kMiB - 1); }
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
 size_t gguf_row_bytes(int dtype, int64_t k) {
   const TypeInfo ti = type_info(dtype);
   return (size_t)(k / ti.bs) * ti.ts;
@@ -102,7 +116,7 @@ int check_weight_shape(int dtype, int64_t n, int64_t k, size_t nbytes) {
 
 int alloc_weight(mq_ctx *ctx, mq_qtensor *t) {
   const size_t bytes = (size_t)t->geo.bytes;
-  const size_t aligned_used = (ctx->arena_used + 255) & ~size_t(255);
+  const size_t aligned_used = align256(ctx->arena_used);
   if (ctx->arena && aligned_used + bytes <= ctx->arena_size) {
     t->data = ctx->arena + aligned_used;
     t->in_arena = true;
@@ -115,82 +129,187 @@ int alloc_weight(mq_ctx *ctx, mq_qtensor *t) {
   return MQ_OK;
 }
 
-int ensure_scratch(mq_ctx *ctx, size_t bytes) {
-  if (bytes <= ctx->scratch_size) return MQ_OK;
-  if (ctx->scratch) {
-    // earlier work on any stream may still read the old buffer
-    HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize before scratch growth");
-    HIP_TRY(hipFree(ctx->scratch), "hipFree scratch");
-    ctx->scratch = nullptr;
-    ctx->scratch_size = 0;
+// The workspace of stream s, at least `bytes` long.  Growth allocates a new
+// buffer and retires the old one (no synchronization, no free).  A stream
+// being captured into a graph cannot grow its workspace.
+int stream_workspace(mq_ctx *ctx, hipStream_t s, size_t bytes, uint8_t **out) {
+  *out = nullptr;
+  mq_ctx::Ws *w = nullptr;
+  for (auto &e : ctx->ws)
+    if (e.stream == s) w = &e;
+  if (!w) {
+    ctx->ws.push_back(mq_ctx::Ws{s, nullptr, 0});
+    w = &ctx->ws.back();
   }
-  const size_t sz = (bytes + (1 << 20) - 1) & ~size_t((1 << 20) - 1);
-  hipError_t e = hipMalloc(&ctx->scratch, sz);
-  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) for scratch failed: %s", sz, hipGetErrorString(e));
-  ctx->scratch_size = sz;
+  if (bytes <= w->size && w->p) {
+    *out = w->p;
+    return MQ_OK;
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(MQ_E_INVALID,
+                "stream is being captured and its workspace (%zu bytes) is smaller than the %zu bytes this call "
+                "needs: run the call once on this stream before capturing or reserve the workspace with "
+                "mq_ctx_reserve_stream_scratch",
+                w->size, bytes);
+  const size_t sz = round_mib(std::max({bytes, 2 * w->size, ctx->ws_floor}));
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) for the stream workspace failed: %s", sz, hipGetErrorString(e));
+  if (w->p) ctx->retired.push_back(w->p);
+  w->p = static_cast<uint8_t *>(p);
+  w->size = sz;
+  *out = w->p;
   return MQ_OK;
 }
 
 WView view_of(const mq_qtensor *w) { return make_view(w->data, w->geo); }
 
-// The stream's tail-partial buffer of at least `bytes`, or NULL when the
-// context already serves kTailStreams other streams (the GEMM then runs every
-// tile whole) or the allocation fails.
-float *tail_buffer(mq_ctx *ctx, hipStream_t s, size_t bytes) {
-  mq_ctx::StreamBuf *b = nullptr;
-  for (int i = 0; i < ctx->tail_used; ++i)
-    if (ctx->tail[i].stream == s) b = &ctx->tail[i];
-  if (!b) {
-    if (ctx->tail_used == mq_ctx::kTailStreams) return nullptr;
-    b = &ctx->tail[ctx->tail_used++];
-    b->stream = s;
+// Scratch layout of one quantized-matmul call.
+struct Plan {
+  bool gemv = false;
+  bool stage_gemm = false;  // f32 (or unaligned bf16) x staged as bf16 for the GEMM
+  bool stage_gemv = false;  // x widened / copied to contiguous f32 for the generic GEMV
+  int64_t kp = 0;           // staged GEMM row length (k rounded up to 64)
+  GemmTail tail{0, 1};
+  size_t stage_off = 0, stage_bytes = 0;
+  size_t part_off = 0, part_bytes = 0;  // GEMM tail partials or generic-GEMV K-split partials
+  size_t total = 0;
+};
+
+Plan plan_qmatmul(const mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
+                  bool gated) {
+  Plan p;
+  const int64_t n = w->n, k = w->k;
+  if (m <= kGemvMaxM && !gated) {
+    p.gemv = true;
+    if (gemv_reads_x_in_place(w->dtype, m, n, k, x, x_dtype, ldx, ctx->cu_count)) return p;  // no scratch
+    p.stage_gemv = x_dtype == MQ_BF16 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 || (ldx % 4) != 0;
+    p.part_bytes = gemv_scratch_bytes(w->dtype, m, n, k, ctx->cu_count);
+    p.stage_bytes = p.stage_gemv ? (size_t)m * k * sizeof(float) : 0;
+  } else {
+    p.kp = (k + 63) / 64 * 64;
+    p.stage_gemm =
+        !(x_dtype == MQ_BF16 && k == p.kp && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0);
+    const int64_t lda = p.stage_gemm ? p.kp : ldx;
+    p.stage_bytes = p.stage_gemm ? (size_t)m * p.kp * sizeof(__bf16) : 0;
+    p.tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
+    if (p.tail.kparts > 1 && gemm_fast_ok(w->dtype, m, k, lda)) p.part_bytes = gemm_tail_bytes(p.tail, m, n);
+    else p.tail.kparts = 1;
   }
-  if (b->size < bytes) {
-    if (b->p) {
-      if (hipStreamSynchronize(s) != hipSuccess) return nullptr;  // earlier work on s may still read it
-      (void)hipFree(b->p);
-      b->p = nullptr;
-      b->size = 0;
-    }
-    const size_t sz = (bytes + (1 << 20) - 1) & ~size_t((1 << 20) - 1);
-    if (hipMalloc(&b->p, sz) != hipSuccess) {
-      b->p = nullptr;
-      return nullptr;
-    }
-    b->size = sz;
-  }
-  return static_cast<float *>(b->p);
+  p.part_off = align256(p.stage_bytes);
+  p.total = p.part_bytes ? p.part_off + p.part_bytes : p.stage_bytes;
+  return p;
 }
 
-// GEMM: stage activations as bf16 [m, kp] (kp multiple of 64, zero padded)
-// unless bf16 x can be read in place, then the fused dequant-MFMA kernel.
-int run_gemm(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
-             int y_dtype, int64_t ldy, const float *bias, const float *gate, int act, hipStream_t s) {
+// Runs one planned call with its scratch at `ws` (p.total bytes).
+int run_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const Plan &p, uint8_t *ws, const void *x, int x_dtype, int64_t m,
+                int64_t ldx, void *y, int y_dtype, int64_t ldy, const float *bias, const float *gate, int act,
+                hipStream_t s) {
   const WView wv = view_of(w);
   const int64_t n = w->n, k = w->k;
-  const int64_t kp = (k + 63) / 64 * 64;
-  const __bf16 *a = nullptr;
-  int64_t lda = 0;
-  const bool direct = x_dtype == MQ_BF16 && k == kp && (ldx % 8) == 0 &&
-                      (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  if (direct) {
-    a = static_cast<const __bf16 *>(x);
-    lda = ldx;
-  } else {
-    int rc = ensure_scratch(ctx, (size_t)m * kp * sizeof(__bf16));
-    if (rc) return rc;
-    __bf16 *st = static_cast<__bf16 *>(ctx->scratch);
-    hipError_t e = launch_stage_bf16(x, x_dtype, m, k, ldx, st, kp, s);
+  float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.part_off) : nullptr;
+  if (p.gemv) {
+    const void *xf = x;
+    int xt = x_dtype;
+    int64_t ldxf = ldx;
+    if (p.stage_gemv) {
+      float *xs = reinterpret_cast<float *>(ws + p.stage_off);
+      hipError_t e = x_dtype == MQ_BF16
+                         ? launch_widen_bf16(static_cast<const __bf16 *>(x), m, k, ldx, xs, s)
+                         : hipMemcpy2DAsync(xs, k * sizeof(float), x, ldx * sizeof(float), k * sizeof(float), m,
+                                            hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) return hip_fail(e, "stage activations for the GEMV");
+      xf = xs;
+      xt = MQ_F32;
+      ldxf = k;
+    }
+    hipError_t e = launch_gemv(w->dtype, wv, n, k, xf, xt, m, ldxf, y, y_dtype, ldy, bias, act, partial,
+                               ctx->cu_count, s);
+    if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    return MQ_OK;
+  }
+  const __bf16 *a = static_cast<const __bf16 *>(x);
+  int64_t lda = ldx;
+  if (p.stage_gemm) {
+    __bf16 *st = reinterpret_cast<__bf16 *>(ws + p.stage_off);
+    hipError_t e = launch_stage_bf16(x, x_dtype, m, k, ldx, st, p.kp, s);
     if (e != hipSuccess) return hip_fail(e, "stage activations");
     a = st;
-    lda = kp;
+    lda = p.kp;
   }
-  GemmTail tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
-  float *partial = nullptr;
-  if (tail.kparts > 1 && gemm_fast_ok(w->dtype, m, k, lda)) partial = tail_buffer(ctx, s, gemm_tail_bytes(tail, m, n));
-  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, tail,
+  hipError_t e = launch_gemm(w->dtype, wv, n, k, w->geo.ntiles, a, m, lda, y, y_dtype, ldy, bias, gate, act, p.tail,
                              partial, s);
   if (e != hipSuccess) return hip_fail(e, "gemm launch");
+  return MQ_OK;
+}
+
+int check_qmatmul_args(const char *fn, const mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m,
+                       int64_t ldx, const void *y, int y_dtype, int64_t ldy, int act) {
+  if (!ctx || !w) return fail(MQ_E_INVALID, "%s: NULL ctx or weight", fn);
+  if (m < 0) return fail(MQ_E_INVALID, "%s: m=%lld < 0", fn, (long long)m);
+  if (m == 0) return MQ_OK;
+  if (!x || !y) return fail(MQ_E_INVALID, "%s: NULL x or y", fn);
+  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: x dtype %d must be F32 or BF16", fn, x_dtype);
+  if (y_dtype != MQ_F32 && y_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: y dtype %d must be F32 or BF16", fn, y_dtype);
+  if (ldx < w->k) return fail(MQ_E_INVALID, "%s: ldx=%lld < k=%lld", fn, (long long)ldx, (long long)w->k);
+  if (ldy < w->n) return fail(MQ_E_INVALID, "%s: ldy=%lld < n=%lld", fn, (long long)ldy, (long long)w->n);
+  if (act != MQ_ACT_NONE && act != MQ_ACT_GELU_TANH) return fail(MQ_E_INVALID, "%s: unknown act %d", fn, act);
+  return MQ_OK;
+}
+
+int make_tensor(mq_ctx *ctx, int dtype, int64_t n, int64_t k, mq_qtensor **out) {
+  mq_qtensor *t = new (std::nothrow) mq_qtensor();
+  if (!t) return fail(MQ_E_OOM, "out of host memory");
+  t->ctx = ctx;
+  t->dtype = dtype;
+  t->n = n;
+  t->k = k;
+  t->geo = make_geo(dtype, n, k);
+  t->gguf_bytes = gguf_row_bytes(dtype, k) * (size_t)n;
+  int rc = alloc_weight(ctx, t);
+  if (rc != MQ_OK) {
+    delete t;
+    return rc;
+  }
+  *out = t;
+  return MQ_OK;
+}
+
+// Raw GGUF blocks already in device memory (at `raw`) into a new
+// device-resident tensor, on stream s.  The repack kernel writes every byte
+// of the tiled layout, padding rows included.
+int tensor_from_raw(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *raw, hipStream_t s, mq_qtensor **out) {
+  mq_qtensor *t = nullptr;
+  int rc = make_tensor(ctx, dtype, n, k, &t);
+  if (rc) return rc;
+  hipError_t e = launch_repack(dtype, raw, t->data, t->geo, false, s);
+  if (e != hipSuccess) {
+    mq_qtensor_free(t);
+    return hip_fail(e, "repack to device layout");
+  }
+  *out = t;
+  return MQ_OK;
+}
+
+// The context's device staging buffer for raw blocks, at least `bytes` long.
+// Callers have synchronized the work that used it before (uploads, quantize
+// and download all return finished).
+int device_stage(mq_ctx *ctx, size_t bytes, uint8_t **out) {
+  if (bytes > ctx->dstage_size) {
+    if (ctx->dstage) {
+      HIP_TRY(hipFree(ctx->dstage), "free upload staging");
+      ctx->dstage = nullptr;
+      ctx->dstage_size = 0;
+    }
+    const size_t sz = round_mib(bytes);
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) for upload staging failed: %s", sz, hipGetErrorString(e));
+    ctx->dstage = static_cast<uint8_t *>(p);
+    ctx->dstage_size = sz;
+  }
+  *out = ctx->dstage;
   return MQ_OK;
 }
 
@@ -244,9 +363,13 @@ void mq_ctx_destroy(mq_ctx *ctx) {
   if (!ctx) return;
   DeviceGuard g(ctx->device);
   (void)hipDeviceSynchronize();
-  if (ctx->scratch) (void)hipFree(ctx->scratch);
-  for (int i = 0; i < ctx->tail_used; ++i)
-    if (ctx->tail[i].p) (void)hipFree(ctx->tail[i].p);
+  for (auto &w : ctx->ws)
+    if (w.p) (void)hipFree(w.p);
+  for (void *p : ctx->retired) (void)hipFree(p);
+  if (ctx->dstage) (void)hipFree(ctx->dstage);
+  for (auto *p : ctx->pinned)
+    if (p) (void)hipHostFree(p);
+  if (ctx->upload_stream) (void)hipStreamDestroy(ctx->upload_stream);
   if (ctx->arena) (void)hipFree(ctx->arena);
   delete ctx;
 }
@@ -267,25 +390,21 @@ int mq_ctx_reserve_arena(mq_ctx *ctx, size_t bytes) {
 int mq_ctx_reserve_scratch(mq_ctx *ctx, size_t bytes) {
   if (!ctx) return fail(MQ_E_INVALID, "ctx is NULL");
   DeviceGuard g(ctx->device);
-  return ensure_scratch(ctx, bytes);
+  ctx->ws_floor = std::max(ctx->ws_floor, bytes);
+  for (size_t i = 0; i < ctx->ws.size(); ++i) {
+    uint8_t *p = nullptr;
+    int rc = stream_workspace(ctx, ctx->ws[i].stream, bytes, &p);
+    if (rc) return rc;
+  }
+  uint8_t *p = nullptr;
+  return stream_workspace(ctx, nullptr, bytes, &p);  // the null stream's, now
 }
 
-static int make_tensor(mq_ctx *ctx, int dtype, int64_t n, int64_t k, mq_qtensor **out) {
-  mq_qtensor *t = new (std::nothrow) mq_qtensor();
-  if (!t) return fail(MQ_E_OOM, "out of host memory");
-  t->ctx = ctx;
-  t->dtype = dtype;
-  t->n = n;
-  t->k = k;
-  t->geo = make_geo(dtype, n, k);
-  t->gguf_bytes = gguf_row_bytes(dtype, k) * (size_t)n;
-  int rc = alloc_weight(ctx, t);
-  if (rc != MQ_OK) {
-    delete t;
-    return rc;
-  }
-  *out = t;
-  return MQ_OK;
+int mq_ctx_reserve_stream_scratch(mq_ctx *ctx, void *stream, size_t bytes) {
+  if (!ctx) return fail(MQ_E_INVALID, "ctx is NULL");
+  DeviceGuard g(ctx->device);
+  uint8_t *p = nullptr;
+  return stream_workspace(ctx, static_cast<hipStream_t>(stream), bytes, &p);
 }
 
 int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *dev_blocks, size_t nbytes,
@@ -295,18 +414,7 @@ int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const v
   int rc = check_weight_shape(dtype, n, k, nbytes);
   if (rc) return rc;
   DeviceGuard g(ctx->device);
-  mq_qtensor *t = nullptr;
-  rc = make_tensor(ctx, dtype, n, k, &t);
-  if (rc) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = hipMemsetAsync(t->data, 0, (size_t)t->geo.bytes, s);
-  if (e == hipSuccess) e = launch_repack(dtype, dev_blocks, t->data, t->geo, false, s);
-  if (e != hipSuccess) {
-    mq_qtensor_free(t);
-    return hip_fail(e, "repack to device layout");
-  }
-  *out = t;
-  return MQ_OK;
+  return tensor_from_raw(ctx, dtype, n, k, dev_blocks, static_cast<hipStream_t>(stream), out);
 }
 
 int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *host_blocks, size_t nbytes,
@@ -316,18 +424,13 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
   int rc = check_weight_shape(dtype, n, k, nbytes);
   if (rc) return rc;
   DeviceGuard g(ctx->device);
-  void *staging = nullptr;
-  hipError_t e = hipMalloc(&staging, nbytes);
-  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) staging failed: %s", nbytes, hipGetErrorString(e));
-  e = hipMemcpy(staging, host_blocks, nbytes, hipMemcpyHostToDevice);
-  if (e != hipSuccess) {
-    (void)hipFree(staging);
-    return hip_fail(e, "hipMemcpy H2D");
-  }
-  rc = mq_qtensor_from_device(ctx, dtype, n, k, staging, nbytes, nullptr, out);
-  hipError_t se = hipStreamSynchronize(nullptr);
-  (void)hipFree(staging);
+  uint8_t *st = nullptr;
+  rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;
+  HIP_TRY(hipMemcpy(st, host_blocks, nbytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  rc = tensor_from_raw(ctx, dtype, n, k, st, nullptr, out);
+  if (rc) return rc;
+  hipError_t se = hipStreamSynchronize(nullptr);
   if (se != hipSuccess) {
     mq_qtensor_free(*out);
     *out = nullptr;
@@ -348,16 +451,14 @@ int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, 
   DeviceGuard g(ctx->device);
   const size_t nbytes = gguf_row_bytes(dtype, k) * (size_t)n;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  void *staging = nullptr;
-  hipError_t e = hipMalloc(&staging, nbytes);
-  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) staging failed: %s", nbytes, hipGetErrorString(e));
-  e = launch_quantize(dtype, src, ld, n, k, staging, s);
-  int rc = MQ_OK;
-  if (e != hipSuccess) rc = hip_fail(e, "quantize launch");
-  if (rc == MQ_OK) rc = mq_qtensor_from_device(ctx, dtype, n, k, staging, nbytes, stream, out);
+  uint8_t *st = nullptr;
+  int rc = device_stage(ctx, nbytes, &st);
+  if (rc) return rc;
+  hipError_t e = launch_quantize(dtype, src, ld, n, k, st, s);
+  if (e != hipSuccess) return hip_fail(e, "quantize launch");
+  rc = tensor_from_raw(ctx, dtype, n, k, st, s, out);
+  if (rc) return rc;
   const hipError_t se = hipStreamSynchronize(s);
-  (void)hipFree(staging);
-  if (rc != MQ_OK) return rc;
   if (se != hipSuccess) {
     mq_qtensor_free(*out);
     *out = nullptr;
@@ -370,13 +471,12 @@ int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, siz
   if (!ctx || !w || !host_blocks) return fail(MQ_E_INVALID, "mq_qtensor_download: NULL argument");
   if (nbytes != w->gguf_bytes) return fail(MQ_E_INVALID, "download needs %zu bytes, got %zu", w->gguf_bytes, nbytes);
   DeviceGuard g(ctx->device);
-  void *staging = nullptr;
-  hipError_t e = hipMalloc(&staging, nbytes);
-  if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) staging failed", nbytes);
-  e = launch_repack(w->dtype, w->data, staging, w->geo, true, nullptr);
+  uint8_t *st = nullptr;
+  int rc = device_stage(ctx, nbytes, &st);
+  if (rc) return rc;
+  hipError_t e = launch_repack(w->dtype, w->data, st, w->geo, true, nullptr);
   if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
-  if (e == hipSuccess) e = hipMemcpy(host_blocks, staging, nbytes, hipMemcpyDeviceToHost);
-  (void)hipFree(staging);
+  if (e == hipSuccess) e = hipMemcpy(host_blocks, st, nbytes, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_fail(e, "download");
   return MQ_OK;
 }
@@ -412,74 +512,116 @@ int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, vo
   return MQ_OK;
 }
 
+int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int64_t m, int gated, size_t *bytes) {
+  if (!ctx || !w || !bytes) return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: NULL argument");
+  if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: m=%lld < 0", (long long)m);
+  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
+    return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: x dtype %d must be F32 or BF16", x_dtype);
+  // a misaligned x pointer takes every staging path, so this is the bound
+  // over all x placements and strides
+  const void *worst = reinterpret_cast<const void *>(uintptr_t(1));
+  *bytes = m == 0 ? 0 : plan_qmatmul(ctx, w, worst, x_dtype, m, w->k, gated != 0).total;
+  return MQ_OK;
+}
+
 int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
                int y_dtype, int64_t ldy, const float *bias, int act, void *stream) {
-  if (!ctx || !w) return fail(MQ_E_INVALID, "mq_qmatmul: NULL ctx or weight");
-  if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul: m=%lld < 0", (long long)m);
-  if (m == 0) return MQ_OK;
-  if (!x || !y) return fail(MQ_E_INVALID, "mq_qmatmul: NULL x or y");
-  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16) return fail(MQ_E_INVALID, "mq_qmatmul: x dtype %d must be F32 or BF16", x_dtype);
-  if (y_dtype != MQ_F32 && y_dtype != MQ_BF16) return fail(MQ_E_INVALID, "mq_qmatmul: y dtype %d must be F32 or BF16", y_dtype);
-  if (ldx < w->k) return fail(MQ_E_INVALID, "mq_qmatmul: ldx=%lld < k=%lld", (long long)ldx, (long long)w->k);
-  if (ldy < w->n) return fail(MQ_E_INVALID, "mq_qmatmul: ldy=%lld < n=%lld", (long long)ldy, (long long)w->n);
-  if (act != MQ_ACT_NONE && act != MQ_ACT_GELU_TANH) return fail(MQ_E_INVALID, "mq_qmatmul: unknown act %d", act);
+  int rc = check_qmatmul_args("mq_qmatmul", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
+  if (rc || m == 0) return rc;
   DeviceGuard g(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const WView wv = view_of(w);
-  const int64_t n = w->n, k = w->k;
-
-  if (m <= kGemvMaxM) {
-    if (gemv_reads_x_in_place(w->dtype, m, n, k, x, x_dtype, ldx, ctx->cu_count)) {
-      // Q4_K: f32 or bf16 x read in place, no scratch
-      hipError_t e = launch_gemv(w->dtype, wv, n, k, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, act, nullptr,
-                                 ctx->cu_count, s);
-      if (e != hipSuccess) return hip_fail(e, "gemv launch");
-      return MQ_OK;
-    }
-    // otherwise x goes to scratch as contiguous f32 (widened from bf16, or
-    // copied when its rows are not 16-byte aligned) unless it already is
-    const void *xf = x;
-    int64_t ldxf = ldx;
-    const bool stage_x = x_dtype == MQ_BF16 || (reinterpret_cast<uintptr_t>(x) & 15) != 0 || (ldx % 4) != 0;
-    size_t need = gemv_scratch_bytes(w->dtype, m, n, k, ctx->cu_count);
-    size_t xoff = (need + 255) & ~size_t(255);
-    if (stage_x) need = xoff + (size_t)m * k * sizeof(float);
-    if (need) {
-      int rc = ensure_scratch(ctx, need);
-      if (rc) return rc;
-    }
-    if (stage_x) {
-      float *xs = reinterpret_cast<float *>(static_cast<uint8_t *>(ctx->scratch) + xoff);
-      hipError_t e = x_dtype == MQ_BF16
-                         ? launch_widen_bf16(static_cast<const __bf16 *>(x), m, k, ldx, xs, s)
-                         : hipMemcpy2DAsync(xs, k * sizeof(float), x, ldx * sizeof(float), k * sizeof(float), m,
-                                            hipMemcpyDeviceToDevice, s);
-      if (e != hipSuccess) return hip_fail(e, "stage activations for the GEMV");
-      xf = xs;
-      ldxf = k;
-    }
-    hipError_t e = launch_gemv(w->dtype, wv, n, k, xf, MQ_F32, m, ldxf, y, y_dtype, ldy, bias, act,
-                               static_cast<float *>(ctx->scratch), ctx->cu_count, s);
-    if (e != hipSuccess) return hip_fail(e, "gemv launch");
-    return MQ_OK;
+  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false);
+  uint8_t *ws = nullptr;
+  if (p.total) {
+    rc = stream_workspace(ctx, s, p.total, &ws);
+    if (rc) return rc;
   }
-
-  return run_gemm(ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
+  return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
 }
 
 int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
                          float *y, int64_t ldy, const float *bias, const float *gate, void *stream) {
-  if (!ctx || !w) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL ctx or weight");
-  if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: m=%lld < 0", (long long)m);
-  if (m == 0) return MQ_OK;
-  if (!x || !y || !gate) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL x, y or gate");
-  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
-    return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: x dtype %d must be F32 or BF16", x_dtype);
-  if (ldx < w->k) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: ldx=%lld < k=%lld", (long long)ldx, (long long)w->k);
-  if (ldy < w->n) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: ldy=%lld < n=%lld", (long long)ldy, (long long)w->n);
+  int rc = check_qmatmul_args("mq_qmatmul_gated_add", ctx, w, x, x_dtype, m, ldx, y, MQ_F32, ldy, MQ_ACT_NONE);
+  if (rc || m == 0) return rc;
+  if (!gate) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL gate");
   DeviceGuard g(ctx->device);
+  hipStream_t s = static_cast<hipStream_t>(stream);
   // every m takes the GEMM kernel: its epilogue holds the gated update
-  return run_gemm(ctx, w, x, x_dtype, m, ldx, y, MQ_F32, ldy, bias, gate, MQ_ACT_NONE, static_cast<hipStream_t>(stream));
+  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, true);
+  uint8_t *ws = nullptr;
+  if (p.total) {
+    rc = stream_workspace(ctx, s, p.total, &ws);
+    if (rc) return rc;
+  }
+  return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, MQ_F32, ldy, bias, gate, MQ_ACT_NONE, s);
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------ GGUF upload
+// Host-side piece of mq_gguf_load_tensor (mq_gguf.cpp): the tensor's bytes go
+// from the file straight into two pinned host buffers in turn, each chunk is
+// copied to the device staging buffer asynchronously (the file read of chunk
+// i+1 overlaps the PCIe copy of chunk i), then the repack runs on the device.
+namespace mq {
+
+int upload_from_file(mq_ctx *ctx, int dtype, int64_t n, int64_t k, int fd, uint64_t offset, size_t nbytes,
+                     mq_qtensor **out) {
+  *out = nullptr;
+  int rc = check_weight_shape(dtype, n, k, nbytes);
+  if (rc) return rc;
+  DeviceGuard g(ctx->device);
+  if (!ctx->upload_stream)
+    HIP_TRY(hipStreamCreateWithFlags(&ctx->upload_stream, hipStreamNonBlocking), "create upload stream");
+  for (auto &p : ctx->pinned)
+    if (!p) HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&p), kUploadChunk, hipHostMallocDefault), "hipHostMalloc");
+  uint8_t *st = nullptr;
+  rc = device_stage(ctx, nbytes, &st);
+  if (rc) return rc;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  for (auto &e : ev)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      for (auto &d : ev)
+        if (d) (void)hipEventDestroy(d);
+      return fail(MQ_E_HIP, "event create failed");
+    }
+  bool used[2] = {false, false};
+  int result = MQ_OK;
+  size_t done = 0;
+  for (int i = 0; done < nbytes; i ^= 1) {
+    const size_t len = std::min(kUploadChunk, nbytes - done);
+    if (used[i] && hipEventSynchronize(ev[i]) != hipSuccess) {  // buffer i's previous copy has left it
+      result = fail(MQ_E_HIP, "upload event wait failed");
+      break;
+    }
+    size_t got = 0;
+    while (got < len) {
+      const ssize_t r = pread(fd, ctx->pinned[i] + got, len - got, (off_t)(offset + done + got));
+      if (r <= 0) break;
+      got += (size_t)r;
+    }
+    if (got != len) {
+      result = fail(MQ_E_IO, "short read at byte %llu of a %zu-byte tensor", (unsigned long long)(offset + done), nbytes);
+      break;
+    }
+    if (hipMemcpyAsync(st + done, ctx->pinned[i], len, hipMemcpyHostToDevice, ctx->upload_stream) != hipSuccess ||
+        hipEventRecord(ev[i], ctx->upload_stream) != hipSuccess) {
+      result = fail(MQ_E_HIP, "async H2D copy failed");
+      break;
+    }
+    used[i] = true;
+    done += len;
+  }
+  if (result == MQ_OK) result = tensor_from_raw(ctx, dtype, n, k, st, ctx->upload_stream, out);
+  const hipError_t se = hipStreamSynchronize(ctx->upload_stream);
+  for (auto &e : ev) (void)hipEventDestroy(e);
+  if (result != MQ_OK) return result;
+  if (se != hipSuccess) {
+    mq_qtensor_free(*out);
+    *out = nullptr;
+    return hip_fail(se, "upload synchronize");
+  }
+  return MQ_OK;
+}
+
+}  // namespace mq

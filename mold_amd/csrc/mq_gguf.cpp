@@ -19,7 +19,11 @@
 #include <string>
 #include <vector>
 
+#include <fcntl.h>
+#include <unistd.h>
+
 #include "../../include/moldq.h"
+#include "mq_internal.h"
 
 namespace {
 
@@ -45,10 +49,6 @@ struct mq_gguf {
   uint64_t alignment = 32;
   std::vector<TensorInfo> tensors;
 };
-
-namespace mq {
-int set_error(int code, const char *msg);  // mq_api.hip: feeds mq_last_error()
-}
 
 namespace {
 
@@ -241,18 +241,12 @@ int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor
     return gfail(MQ_E_UNSUPPORTED, "tensor %s is dense (type %d); only GGUF block types upload", t.name.c_str(), t.dtype);
   int64_t rows = 1;
   for (int d = 1; d < t.n_dims; ++d) rows *= t.dims[d];
-  std::vector<uint8_t> buf;
-  try {
-    buf.resize(t.nbytes);
-  } catch (...) {
-    return gfail(MQ_E_OOM, "cannot allocate %zu host bytes", t.nbytes);
-  }
-  FILE *f = fopen(g->path.c_str(), "rb");
-  if (!f) return gfail(MQ_E_IO, "cannot reopen %s", g->path.c_str());
-  const bool ok = fseeko(f, (off_t)t.offset, SEEK_SET) == 0 && fread(buf.data(), 1, t.nbytes, f) == t.nbytes;
-  fclose(f);
-  if (!ok) return gfail(MQ_E_IO, "short read of tensor %s", t.name.c_str());
-  return mq_qtensor_upload(ctx, t.dtype, rows, t.dims[0], buf.data(), t.nbytes, out);
+  if (!ctx) return gfail(MQ_E_INVALID, "mq_gguf_load_tensor: NULL ctx");
+  const int fd = open(g->path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return gfail(MQ_E_IO, "cannot reopen %s", g->path.c_str());
+  const int rc = mq::upload_from_file(ctx, t.dtype, rows, t.dims[0], fd, t.offset, t.nbytes, out);
+  close(fd);
+  return rc;
 }
 
 }  // extern "C"

@@ -4,8 +4,10 @@
 
 namespace mq {
 
-// One thread per GGUF byte (grid-stride).  inverse=false: raw -> tiled;
-// inverse=true: tiled -> raw.  Upload/download only, never on the hot path.
+// One thread per GGUF byte (grid-stride).  inverse=false: raw -> tiled, over
+// the padded row count so the rows past n of the last tile are written as
+// zeros (no separate clear); inverse=true: tiled -> raw over the n real rows.
+// Upload/download only, never on the hot path.
 template <int TYPE>
 __global__ void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, Geo g,
                               int64_t total, int inverse) {
@@ -24,14 +26,14 @@ __global__ void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restri
     const int64_t off = field_offset(g.plane[f], ti.f[f].size, g.nb, n / kRowTile, b,
                                      (int)(n % kRowTile), j - ti.f[f].off);
     if (inverse) dst[i] = src[off];
-    else dst[off] = src[i];
+    else dst[off] = n < g.n ? src[i] : uint8_t(0);
   }
 }
 
 hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, bool inverse,
                          hipStream_t stream) {
   const TypeInfo ti = type_info(type);
-  const int64_t total = g.n * g.nb * ti.ts;
+  const int64_t total = (inverse ? g.n : g.ntiles * kRowTile) * g.nb * ti.ts;
   if (total == 0) return hipSuccess;
   const int threads = 256;
   const int64_t want = (total + threads - 1) / threads;

@@ -85,7 +85,12 @@ class Device:
         check(_lib.load().mq_ctx_reserve_arena(self._h, nbytes))
 
     def reserve_scratch(self, nbytes: int) -> None:
+        """Minimum size of every stream's workspace (staging + split-K partials)."""
         check(_lib.load().mq_ctx_reserve_scratch(self._h, nbytes))
+
+    def reserve_stream_scratch(self, nbytes: int, stream=None) -> None:
+        """Grow one stream's workspace now (e.g. before capturing it in a graph)."""
+        check(_lib.load().mq_ctx_reserve_stream_scratch(self._h, _stream_ptr(stream), nbytes))
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -214,6 +219,15 @@ class QMatMul:
     @classmethod
     def from_qtensor(cls, w: QTensor) -> "QMatMul":
         return cls(w)
+
+    def workspace_bytes(self, m: int, x_dtype=None, gated: bool = False) -> int:
+        """Stream workspace a call with `m` rows needs (the bound over x placements)."""
+        torch = _torch()
+        out = ctypes.c_size_t()
+        check(_lib.load().mq_qmatmul_workspace_size(self.w.device.handle, self.w.handle,
+                                                    _dtype_code(x_dtype or torch.float32), int(m), int(gated),
+                                                    ctypes.byref(out)))
+        return out.value
 
     def forward(self, x, bias=None, act: int = ACT_NONE, out_dtype=None, out=None, stream=None):
         torch = _torch()
