@@ -140,6 +140,20 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
                int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
                const float *bias, int act, void *stream);
 
+/* mq_qmatmul that allocates nothing, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+ * kernels and results as mq_qmatmul; its scratch (activation staging and
+ * split-K partials) is one fixed 64 MiB device array per GPU, held until the
+ * process ends.  A call whose scratch would exceed it fails with
+ * MQ_E_INVALID (mq_qmatmul_workspace_size gives the need; bf16 x with 16-byte
+ * aligned rows needs only the partials).  Every call on one GPU shares that
+ * array: calls that overlap in time on one GPU (other streams, other
+ * contexts, other threads) race and must be ordered by the caller. */
+int mq_qmatmul_noalloc(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
+                       int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
+                       const float *bias, int act, void *stream);
+
 /* --- Block glue between the quantized linears (fused row passes).  Both are
  *     asynchronous on `stream` and allocate nothing. -------------------------- */
 

@@ -16,6 +16,10 @@
 
 using namespace mq;
 
+// Scratch of mq_qmatmul_noalloc: one copy per GPU, reached from host code only
+// through the per-device address that mq_ctx_create resolves (noalloc_scratch).
+static __device__ __align__(256) uint8_t scratch[MQ_NOALLOC_SCRATCH_BYTES];
+
 struct mq_ctx {
   int device = 0;
   int cu_count = 0;
@@ -42,6 +46,8 @@ struct mq_ctx {
   size_t dstage_size = 0;
   uint8_t *pinned[2] = {nullptr, nullptr};
   hipStream_t upload_stream = nullptr;
+  // Device address of this GPU's copy of `scratch` (mq_qmatmul_noalloc).
+  uint8_t *noalloc_scratch = nullptr;
 };
 
 struct mq_qtensor {
@@ -351,10 +357,16 @@ int mq_ctx_create(int device_ordinal, mq_ctx **out) {
   if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(MQ_E_UNSUPPORTED, "device %d is %s; this library is built for gfx950 only", device_ordinal,
                 prop.gcnArchName);
+  void *sp = nullptr;
+  {
+    DeviceGuard g(device_ordinal);
+    HIP_TRY(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+  }
   mq_ctx *c = new (std::nothrow) mq_ctx();
   if (!c) return fail(MQ_E_OOM, "out of host memory");
   c->device = device_ordinal;
   c->cu_count = prop.multiProcessorCount;
+  c->noalloc_scratch = static_cast<uint8_t *>(sp);
   *out = c;
   return MQ_OK;
 }
@@ -537,6 +549,24 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
     if (rc) return rc;
   }
   return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
+}
+
+int mq_qmatmul_noalloc(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
+                       int y_dtype, int64_t ldy, const float *bias, int act, void *stream) {
+  int rc = check_qmatmul_args("mq_qmatmul_noalloc", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
+  if (rc || m == 0) return rc;
+  DeviceGuard g(ctx->device);
+  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false);
+  if (p.total > MQ_NOALLOC_SCRATCH_BYTES)
+    return fail(MQ_E_INVALID,
+                "mq_qmatmul_noalloc: this call needs %zu bytes of scratch, more than its fixed %zu bytes "
+                "(fewer rows, or bf16 x with 16-byte aligned rows, need less; mq_qmatmul has no limit)",
+                p.total, (size_t)MQ_NOALLOC_SCRATCH_BYTES);
+  // Every scratch byte the kernels read is written earlier in the same call
+  // (staged rows and their zero padding, every split-K partial), so nothing
+  // is cleared first.
+  return run_qmatmul(ctx, w, p, ctx->noalloc_scratch, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act,
+                     static_cast<hipStream_t>(stream));
 }
 
 int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,

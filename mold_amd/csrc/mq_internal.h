@@ -7,6 +7,10 @@
 
 #include "../../include/moldq.h"
 
+// Size of the file-scope device array that mq_qmatmul_noalloc uses as its
+// scratch (one copy per GPU, held until the process ends).
+#define MQ_NOALLOC_SCRATCH_BYTES (size_t(64) << 20)
+
 namespace mq {
 
 // Pinned host chunk of the file -> HBM weight upload (two are used in turn).
