@@ -1,22 +1,42 @@
 """Benchmark of the GGUF quantized-linear hot path on one MI355X.
 
 Headline (the `value`): the fused dequant -> bf16-MFMA GEMM of a Q4_K weight
-at FLUX single-block linear1 shape, x f32 [4608, 3072] . W[21504, 3072]^T ->
+at FLUX single-block linear1 shape, x [4608, 3072] . W[21504, 3072]^T ->
 y f32 [4608, 21504] (the shape the north star's
->= 50 % of bf16 MFMA peak target names).  One step = one QMatMul::forward
-call over that batch: activation staging f32 -> bf16 plus the GEMM kernel.
-`value` = 2*M*N*K / (ms_per_step) in TFLOP/s.
+>= 50 % of bf16 MFMA peak target names).  x is bf16 and resident in HBM: that
+is what the FLUX step feeds linear1 (its adaLN modulation writes bf16).  One
+step = one QMatMul::forward call = exactly one GEMM kernel launch, so the
+HIP-event time over the timed launches (roofline.kernel_ms, on the launch
+stream) is that kernel's average duration, and ms_per_step is the host wall
+clock around the same launches.  `value` = 2*M*N*K / ms_per_step in TFLOP/s.
+Before the W warmup steps the GEMM runs for one second untimed, so that the
+timed steps see the chip's steady, power-limited clock rather than its ramp.
 
-Also reported on the same JSON line:
-  * "roofline": the GEMM kernel alone (bf16 activations already staged, so
-    each launch is exactly one gemm kernel), timed with HIP events on the
-    launch stream, against the 2.5 PFLOP/s dense bf16 MFMA peak;
+Also on the same JSON line:
+  * "roofline": that kernel against the 2.5 PFLOP/s dense bf16 MFMA peak;
+    `traffic` (HBM bytes per launch) comes from the committed counter summary
+    profiles/gemm_q4k_linear1_traffic.md only when the kernel sources' digest
+    recorded there matches the sources of this build (else null);
+  * "f32_input": the same call with f32 x (candle's QMatMul input dtype):
+    staging to bf16 plus the GEMM;
+  * "config1_q8_0": BASELINE config 1, the Q8_0 3072x3072 out-projection at
+    M=4608 with f32 x and y;
+  * "config3_mlp": BASELINE config 3, the MLP chain fc1 (3072->12288, GELU-tanh
+    epilogue, bf16 out) then fc2 (12288->3072, f32 out) on f32 x [4608, 3072],
+    for Q4_K, Q4_0 and Q6_K weights;
+  * "dequant": QTensor::dequantize of a Q4_K 18432x3072 weight to f32 and to
+    bf16, in GB/s of algorithmic bytes (GGUF blocks read + dense out written);
   * "gemv": the skinny-M Q4_K modulation GEMVs (config 2, M in {1, 2, 4},
     N in {18432, 9216}), rotating through > 256 MB of distinct weight copies
     so reads miss the Infinity Cache, in GB/s of algorithmic bytes against
     the 8 TB/s HBM peak.  The rotation is captured once in a HIP graph and
     replayed, so the figure is the kernels' own rate, not Python's launch
     rate;
+  * "dense_bf16_ceiling": torch's bf16 linear (hipBLASLt) at the headline shape
+    with a dense bf16 weight, the achievable-MFMA reference;
+  * "upload": GGUF file -> HBM rate of mq_gguf_load_tensor (pinned,
+    double-buffered) over a 300 MB file just written (so read from the page
+    cache: PCIe and the pipeline, not the disk), and of the host-buffer upload;
   * "flux_step": one FLUX.1-dev-shaped denoising-step forward at 1024^2
     (19 double + 38 single blocks, hidden 3072,
     4096 image + 512 text tokens, every linear Q4_K except the bf16 img_in),
@@ -30,16 +50,13 @@ Also reported on the same JSON line:
     block 0 and the output layer on the CPU, extrapolated x60);
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
-    oracle/ and timed on a bounded row sample of the same workload on this
-    host's cores.
+    oracle/, timed on a bounded row sample of the headline workload on this
+    host's cores for the portable build and for a -march=native build
+    compiled on this host (the faster is `value`), with the CPU model named.
 
 Weights are N(0, 0.02^2) quantized to GGUF blocks on the GPU by libmoldq's
-quantizer when available; activations are N(0, 1) from torch's seeded
-generator.  Everything is resident in HBM before the timed region.
-HBM traffic per GEMM launch ("roofline.traffic") comes from the committed
-rocprofv3 counter summary profiles/gemm_q4k_linear1_traffic.md (FETCH_SIZE and
-WRITE_SIZE of `python3 bench.py --pmc-pass`, each scaled by what the counter
-reads for a plain copy of known size in the same run); null if absent.
+quantizer; activations are N(0, 1) from torch's seeded generator.
+Everything is resident in HBM before each timed region.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv] [--no-flux] [--no-qwen]
        python bench.py --pmc-pass     (few launches of each kernel, for counters)
@@ -49,10 +66,12 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-gemv
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import re
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -61,12 +80,33 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-GEMM_KERNEL = "mq::gemm_fast_kernel<12, float>"   # Q4_K weights, f32 output
+GEMM_KERNEL = "mq::gemm_fast_kernel<12, float, false>"   # Q4_K weights, f32 output, no gated epilogue
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_q4k_linear1_traffic.md")
+GEMM_SOURCES = ["mq_gemm.hip", "mq_bfrag.h", "mq_kernels.h", "mq_common.h"]
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gemm_source_digest() -> str:
+    """sha256 (first 16 hex digits) over the GEMM kernel's source files."""
+    h = hashlib.sha256()
+    for name in GEMM_SOURCES:
+        with open(os.path.join(ROOT, "mold_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def make_weight(dev, dtype, n, k, seed):
@@ -80,15 +120,29 @@ def make_weight(dev, dtype, n, k, seed):
     return qt
 
 
-def time_events(fn, iters):
+def timed(fn, steps, warmup=0, prewarm_s=0.0):
+    """Run fn `prewarm_s` seconds and `warmup` times untimed, then `steps` times
+    between two synchronizations: returns (wall ms per step, HIP-event ms per
+    step on the current stream over the same launches)."""
     import torch
+    if prewarm_s > 0:
+        t_end = time.perf_counter() + prewarm_s
+        while time.perf_counter() < t_end:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+    for _ in range(warmup):
+        fn()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     s.record()
-    for _ in range(iters):
+    for _ in range(steps):
         fn()
     e.record()
-    e.synchronize()
-    return s.elapsed_time(e) / iters  # ms
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, s.elapsed_time(e) / steps
 
 
 def bench_gemm(dev, args):
@@ -101,35 +155,149 @@ def bench_gemm(dev, args):
     mm = mold_amd.QMatMul(qt)
     g = torch.Generator(device="cuda").manual_seed(40)
     x = torch.randn((m, k), device="cuda", generator=g)
-    y = torch.empty((m, n), device="cuda", dtype=torch.float32)
-    dev.reserve_scratch(m * k * 2)
-    flop = 2.0 * m * n * k
-    log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        mm.forward(x, out=y)
-    torch.cuda.synchronize()
-    log(f"timing {args.steps} steps")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        mm.forward(x, out=y)
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    assert not torch.isnan(y).any().item(), "NaN in GEMM output"
-    # dominant kernel alone: bf16 activations are consumed in place
     xb = x.to(torch.bfloat16)
-    for _ in range(2):
-        mm.forward(xb, out=y)
-    kern_ms = time_events(lambda: mm.forward(xb, out=y), args.steps)
+    y = torch.empty((m, n), device="cuda", dtype=torch.float32)
+    flop = 2.0 * m * n * k
+    log(f"pre-warm 1 s, warmup {args.warmup}, timing {args.steps} steps")
+    wall_ms, kern_ms = timed(lambda: mm.forward(xb, out=y), args.steps, args.warmup, prewarm_s=1.0)
+    assert torch.isfinite(y).all().item(), "non-finite GEMM output"
+    f32_wall, f32_ev = timed(lambda: mm.forward(x, out=y), max(20, args.steps // 4), 3)
     res = {
         "ms_per_step": wall_ms,
         "tflops": flop / (wall_ms * 1e-3) / 1e12,
         "kernel_ms": kern_ms,
         "kernel_tflops": flop / (kern_ms * 1e-3) / 1e12,
         "flop": flop,
+        "f32_input": {"ms": round(f32_ev, 4), "tflops": round(flop / (f32_ev * 1e-3) / 1e12, 1),
+                      "frac": round(flop / (f32_ev * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                      "what": "QMatMul::forward with f32 x [4608,3072]: f32->bf16 staging kernel + the GEMM"},
     }
     blocks = qt.data() if not args.no_cpu else None
     return res, blocks, x
+
+
+def bench_config1(dev, args):
+    """Q8_0 3072x3072 at M=4608, f32 x and y."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    m, n, k = 4608, 3072, 3072
+    log("config 1: Q8_0 3072x3072, M=4608")
+    mm = mold_amd.QMatMul(make_weight(dev, GgmlDType.Q8_0, n, k, seed=1))
+    g = torch.Generator(device="cuda").manual_seed(10)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    xb = x.to(torch.bfloat16)
+    y = torch.empty((m, n), device="cuda")
+    flop = 2.0 * m * n * k
+    steps = max(50, args.steps)
+    _, ms = timed(lambda: mm.forward(x, out=y), steps, 5, prewarm_s=0.2)
+    _, kms = timed(lambda: mm.forward(xb, out=y), steps, 5)
+    return {"m": m, "n": n, "k": k, "ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+            "frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "gemm_kernel_ms": round(kms, 4),
+            "gemm_kernel_frac": round(flop / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "what": "f32 x staged to bf16 + fused Q8_0 GEMM (ms, tflops, frac); the GEMM alone on bf16 x "
+                    "(gemm_kernel_*)"}
+
+
+def bench_config3(dev, args):
+    """MLP fc1 + GELU-tanh -> fc2 at M=4608 for three block layouts."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    m, h, f = 4608, 3072, 12288
+    g = torch.Generator(device="cuda").manual_seed(30)
+    x = torch.randn((m, h), device="cuda", generator=g)
+    hid = torch.empty((m, f), device="cuda", dtype=torch.bfloat16)
+    y = torch.empty((m, h), device="cuda")
+    flop = 2.0 * m * h * f * 2
+    out = []
+    for tname in ("Q4_K", "Q4_0", "Q6_K"):
+        t = GgmlDType[tname]
+        log(f"config 3: MLP {tname}")
+        fc1 = mold_amd.QMatMul(make_weight(dev, t, f, h, seed=31))
+        fc2 = mold_amd.QMatMul(make_weight(dev, t, h, f, seed=32))
+
+        def chain():
+            fc1.forward(x, act=mold_amd.ACT_GELU_TANH, out=hid)
+            fc2.forward(hid, out=y)
+        steps = max(20, args.steps // 4)
+        _, ms = timed(chain, steps, 3, prewarm_s=0.2)
+        _, ms1 = timed(lambda: fc1.forward(x, act=mold_amd.ACT_GELU_TANH, out=hid), steps, 2)
+        _, ms2 = timed(lambda: fc2.forward(hid, out=y), steps, 2)
+        out.append({"weight": tname, "ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                    "frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                    "fc1_ms": round(ms1, 4), "fc2_ms": round(ms2, 4)})
+        del fc1, fc2
+    return {"m": m, "hidden": h, "mlp": f, "chains": out,
+            "what": "fc1 3072->12288 (f32 x staged to bf16, GELU-tanh epilogue, bf16 out) then fc2 12288->3072 "
+                    "(bf16 in, f32 out); flop = both GEMMs"}
+
+
+def bench_dequant(dev, args):
+    """QTensor::dequantize of Q4_K 18432x3072 to f32 and bf16, GB/s."""
+    import torch
+    from mold_amd import GgmlDType
+    n, k = 18432, 3072
+    log("dequantize Q4_K 18432x3072")
+    qt = make_weight(dev, GgmlDType.Q4_K, n, k, seed=7)
+    res = {"weight": "Q4_K", "n": n, "k": k, "gguf_bytes": qt.storage_size_in_bytes()}
+    for name, dt, es in (("f32", torch.float32, 4), ("bf16", torch.bfloat16, 2)):
+        out = torch.empty((n, k), device="cuda", dtype=dt)
+        _, ms = timed(lambda: qt.dequantize(dt, out=out), max(20, args.steps // 4), 3, prewarm_s=0.1)
+        nbytes = qt.storage_size_in_bytes() + n * k * es
+        res[name] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    return res
+
+
+def bench_dense_ceiling(args):
+    """torch bf16 linear (hipBLASLt) at the headline shape: the dense-bf16 MFMA ceiling."""
+    import torch
+    m, n, k = 4608, 21504, 3072
+    log("dense bf16 ceiling (torch linear, hipBLASLt)")
+    g = torch.Generator(device="cuda").manual_seed(50)
+    xb = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+    wb = (torch.randn((n, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    out = torch.empty((m, n), device="cuda", dtype=torch.bfloat16)
+    _, ms = timed(lambda: torch.mm(xb, wb.t(), out=out), max(20, args.steps // 2), 5, prewarm_s=0.5)
+    flop = 2.0 * m * n * k
+    return {"ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+            "frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "what": "torch.mm (x . W^T), bf16 x [4608,3072], dense bf16 W [21504,3072], bf16 out"}
+
+
+def bench_upload(dev, args):
+    """GGUF file -> HBM and host buffer -> HBM upload rates."""
+    import numpy as np
+    import mold_amd
+    from mold_amd import GgmlDType, gguf
+    n, k, count = 21504, 3072, 8
+    t = GgmlDType.Q4_K
+    nbytes = n * (k // 256) * 144
+    rng = np.random.default_rng(60)
+    raw = [rng.integers(0, 256, nbytes, dtype=np.uint8) for _ in range(count)]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "w.gguf")
+        gguf.write(path, [(f"blk.{i}.weight", t, (n, k), r) for i, r in enumerate(raw)])
+        log(f"upload: GGUF file {count * nbytes / 1e6:.0f} MB")
+        c = gguf.Content.read(path)
+        c.tensor("blk.0.weight", dev).free()             # first-use setup (pinned buffers, stream)
+        t0 = time.perf_counter()
+        qts = [c.tensor(f"blk.{i}.weight", dev) for i in range(count)]
+        dt_file = time.perf_counter() - t0
+        c.close()
+    ok = all(np.array_equal(q.data(), r) for q, r in zip(qts[:1], raw[:1]))
+    del qts
+    t0 = time.perf_counter()
+    qts = [mold_amd.QTensor.from_blocks(dev, t, (n, k), r) for r in raw]
+    dt_host = time.perf_counter() - t0
+    del qts
+    return {"bytes": count * nbytes, "tensors": count,
+            "gguf_file_gbs": round(count * nbytes / dt_file / 1e9, 2),
+            "host_buffer_gbs": round(count * nbytes / dt_host / 1e9, 2), "readback_identical": bool(ok),
+            "what": "mq_gguf_load_tensor over a freshly written file (page cache: PCIe + pipeline, not disk), "
+                    "pinned 16 MiB chunks double-buffered; host_buffer = mq_qtensor_upload from pageable numpy"}
 
 
 def bench_gemv(dev, args):
@@ -159,7 +327,8 @@ def bench_gemv(dev, args):
             graph.replay()
             torch.cuda.synchronize()
             iters = max(10, args.steps)
-            ms = time_events(graph.replay, iters) / copies
+            _, ms = timed(graph.replay, iters, 2, prewarm_s=0.1)
+            ms /= copies
             nbytes = wbytes + 4 * m * k + 4 * m * n
             out.append({"m": m, "n": n, "k": k, "us": round(ms * 1e3, 3), "bytes": nbytes,
                         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -204,7 +373,8 @@ def bench_flux(dev, args):
            "flop_linear": lin, "flop_attention": attn,
            "weight_bytes": params.quantized_bytes(), "attention": F.ATTENTION_BACKEND["name"],
            "config": "FLUX.1-dev shape, 1024x1024, batch 1, 4096 img + 512 txt tokens, Q4_K linears, "
-                     "f32 activations, bf16 GEMM inputs and attention"}
+                     "f32 activations, bf16 GEMM inputs and attention; attention is PyTorch's fused SDPA "
+                     "(on ROCm AOTriton's precompiled attn_fwd kernel), not part of libmoldq"}
     return res, params, inp
 
 
@@ -245,7 +415,8 @@ def bench_qwen(dev, args):
            "config": f"Qwen-Image shape, 1328x1328, batch 1, {l_img} img + 256 txt tokens, 60 blocks; "
                      "q/k/v Q3_K (stacked per stream), MLP Q2_K, out-projections, modulation, stems Q4_K; "
                      "f32 residuals, bf16 GEMM inputs and attention (joint sequence padded to a multiple of 256 "
-                     "with zero keys, removed exactly), text stream on a second HIP stream"}
+                     "with zero keys, corrected by the log-sum-exp), text stream on a second HIP stream; attention is "
+                     "PyTorch's fused SDPA (on ROCm AOTriton's precompiled attn_fwd kernel), not part of libmoldq"}
     return res, params, inp
 
 
@@ -346,14 +517,20 @@ def cpu_flux_baseline(params, inp):
 
 
 def read_traffic():
-    """HBM bytes per GEMM launch from the committed counter summary, or None."""
+    """HBM bytes per GEMM launch from the committed counter summary, when the
+    summary was taken on these kernel sources (its recorded digest matches);
+    else None."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             text = f.read()
     except OSError:
         return None
     mt = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
-    return int(mt.group(1)) if mt else None
+    md = re.search(r"source_digest:\s*([0-9a-f]{16})", text)
+    if not mt or not md or md.group(1) != gemm_source_digest():
+        log("traffic summary absent or taken on other kernel sources: roofline.traffic = null")
+        return None
+    return int(mt.group(1))
 
 
 def pmc_pass(dev, args):
@@ -363,6 +540,7 @@ def pmc_pass(dev, args):
     import torch
     import mold_amd
     from mold_amd import GgmlDType
+    log(f"kernel source digest {gemm_source_digest()}")
     nbytes = 256 << 20
     a = torch.empty(nbytes // 4, device="cuda").normal_()
     b = torch.empty_like(a)
@@ -388,41 +566,59 @@ def pmc_pass(dev, args):
     log("GEMV launches done")
 
 
-def cpu_baseline(blocks, x, n, k, budget_s=12.0):
-    """candle CPU QMatMul algorithm (oracle restatement) on a row sample."""
+def cpu_baseline(blocks, x, n, k, budget_s=8.0):
+    """candle CPU QMatMul algorithm (oracle restatement) on a row sample, timed for
+    both builds (portable -march=x86-64-v2, and -march=native compiled on this
+    host); `value` is the faster."""
     import numpy as np
     from oracle import oracle as O
     threads = min(16, os.cpu_count() or 1)
-    xs = x[:4].float().cpu().numpy()
-    t0 = time.perf_counter()
-    O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads)
-    per_row = (time.perf_counter() - t0) / 4
-    rows = int(max(4, min(4608, budget_s / max(per_row, 1e-6))))
-    xs = x[:rows].float().cpu().numpy()
-    t0 = time.perf_counter()
-    O.matmul_candle(O.Q4_K, np.ascontiguousarray(xs), blocks, n, k, nthreads=threads)
-    dt = time.perf_counter() - t0
-    return {"value": 2.0 * rows * n * k / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    builds = [("gcc -O3 -march=x86-64-v2", False)]
+    try:
+        O.native_lib()
+        builds.append(("gcc -O3 -march=native", True))
+    except Exception as err:  # no compiler on this host
+        log(f"native oracle build failed ({err}); timing the portable build only")
+    timings = {}
+    for label, native in builds:
+        xs = np.ascontiguousarray(x[:8].float().cpu().numpy())
+        t0 = time.perf_counter()
+        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads, native=native)
+        per_row = (time.perf_counter() - t0) / 8
+        rows = int(max(8, min(4608, budget_s / max(per_row, 1e-6))))
+        xs = np.ascontiguousarray(x[:rows].float().cpu().numpy())
+        t0 = time.perf_counter()
+        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads, native=native)
+        dt = time.perf_counter() - t0
+        timings[label] = (2.0 * rows * n * k / dt / 1e12, rows, dt)
+        log(f"  CPU {label}: {timings[label][0]:.4f} TFLOP/s over {rows} rows ({dt:.1f} s)")
+    best = max(timings, key=lambda lb: timings[lb][0])
+    tf, rows, dt = timings[best]
+    return {"value": tf, "unit": "TFLOP/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
+            "build": best, "all_builds": {lb: round(v[0], 4) for lb, v in timings.items()},
             "sample": f"{rows} of 4608 rows of x [4608,3072] against the full Q4_K W[21504,3072] "
-                      f"({dt:.1f} s; candle CPU algorithm: x->Q8_K, integer block dots, {threads} threads)"}
+                      f"({dt:.1f} s; candle CPU algorithm restated in C: x->Q8_K, integer block dots, "
+                      f"{threads} threads over output columns)"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemv", action="store_true")
     ap.add_argument("--no-flux", action="store_true")
     ap.add_argument("--flux-only", action="store_true")
     ap.add_argument("--no-qwen", action="store_true")
     ap.add_argument("--qwen-only", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1/3, dequant, ceiling and upload legs")
     ap.add_argument("--pmc-pass", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the reference runs one whole model per GPU, with no collectives).", file=sys.stderr)
+        print("bench.py measures one GPU only: every GPU box in this setup has one GPU, and this build has "
+              "no multi-GPU path (the reference runs one whole model per GPU, with no collectives).",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     import mold_amd
@@ -441,8 +637,18 @@ def main():
         print(json.dumps({"qwen_step": qwen}), flush=True)
         return
     gemm, blocks, x = bench_gemm(dev, args)
-    log(f"GEMM: {gemm['ms_per_step']:.3f} ms/step {gemm['tflops']:.1f} TFLOP/s; kernel {gemm['kernel_ms']:.3f} ms "
-        f"{gemm['kernel_tflops']:.1f} TFLOP/s")
+    log(f"GEMM: {gemm['ms_per_step']:.4f} ms/step {gemm['tflops']:.1f} TFLOP/s; kernel {gemm['kernel_ms']:.4f} ms "
+        f"{gemm['kernel_tflops']:.1f} TFLOP/s; f32 input {gemm['f32_input']['ms']:.4f} ms")
+    extra = {}
+    if not args.no_extra:
+        extra["config1_q8_0"] = bench_config1(dev, args)
+        extra["config3_mlp"] = bench_config3(dev, args)
+        extra["dequant"] = bench_dequant(dev, args)
+        extra["dense_bf16_ceiling"] = bench_dense_ceiling(args)
+        extra["upload"] = bench_upload(dev, args)
+        torch.cuda.empty_cache()
+        for key, v in extra.items():
+            log(f"{key}: {json.dumps(v)[:300]}")
     gemv = None if args.no_gemv else bench_gemv(dev, args)
     flux = None
     if not args.no_flux:
@@ -479,15 +685,17 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: W ~ N(0, 0.02^2) quantized to Q4_K on the GPU, x ~ N(0, 1) f32",
+        "data": "synthetic: W ~ N(0, 0.02^2) quantized to Q4_K on the GPU, x ~ N(0, 1) as bf16",
         "config": {"workload": "flux_single_block_linear1_q4k", "m": 4608, "n": 21504, "k": 3072,
-                   "weight": "Q4_K", "x": "f32", "y": "f32"},
+                   "weight": "Q4_K", "x": "bf16", "y": "f32"},
         "roofline": {"bound": "mfma", "achieved": round(gemm["kernel_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gemm["kernel_tflops"] / PEAK_BF16_TFLOPS, 4),
                      "traffic": read_traffic(), "kernel": GEMM_KERNEL,
                      "kernel_ms": round(gemm["kernel_ms"], 4),
-                     "algorithmic_flop_per_launch": gemm["flop"]},
+                     "algorithmic_flop_per_launch": gemm["flop"], "source_digest": gemm_source_digest()},
         "cpu_baseline": cpu,
+        "f32_input": gemm["f32_input"],
+        **extra,
         "gemv": gemv,
         "flux_step": flux,
         "qwen_step": qwen,

@@ -107,7 +107,9 @@ int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
 /* Quantize a dense f32 matrix already on the device, src[n, k] with row
  * stride ld (elements), into a new device-resident GGUF weight of `dtype`.
  * The blocks are byte-identical to ggml's reference quantizers
- * (quantize_row_*_ref), which candle's k_quants port mirrors.  Replaces
+ * (quantize_row_*_ref).  Byte parity with candle's own k-quant quantizers
+ * (Q2_K..Q6_K) is unpinned: candle may use make_qkx1_quants where ggml's
+ * reference uses make_qkx2_quants.  Replaces
  * QTensor::quantize / quantize_onto (crates/mold-inference/src/flux/
  * pipeline.rs:219-229, crates/mold-inference/src/flux/lora.rs:849).
  * Runs on `stream` after work already queued there and returns when the

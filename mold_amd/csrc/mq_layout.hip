@@ -83,8 +83,8 @@ __device__ __forceinline__ void store8<_Float16>(_Float16 *dst, const float v[8]
   *reinterpret_cast<f16x8 *>(dst) = r;
 }
 
-// One thread per 8 consecutive outputs of a row; consecutive threads write
-// consecutive 8-element groups (coalesced stores, the dominant traffic).
+// Fallback for k % 256 != 0 (legacy 32-element types only): one thread per 8
+// consecutive outputs of a row, decoding straight from the tiled layout.
 template <int TYPE, typename OUT>
 __global__ void dequant_kernel(WView w, int64_t n, int64_t k, OUT *__restrict__ dst) {
   constexpr TypeInfo ti = type_info(TYPE);
@@ -102,10 +102,86 @@ __global__ void dequant_kernel(WView w, int64_t n, int64_t k, OUT *__restrict__ 
   }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Blocks of one 256-element column step, and the LDS bytes their records take
+// for one 64-row tile.
+template <int TYPE>
+constexpr int dq_blocks() {
+  return 256 / type_info(TYPE).bs;
+}
+template <int TYPE>
+constexpr int dq_lds_bytes() {
+  return kRowTile * type_info(TYPE).ts * dq_blocks<TYPE>();
+}
+
+// One workgroup per (64-row tile, 256-element column step).  In the tiled
+// layout the records of one tile's consecutive blocks are contiguous in every
+// field plane, so the workgroup first copies them to LDS with coalesced
+// 16-byte loads (each weight byte is read from HBM once), then decodes from
+// LDS with the same decode8 as the other paths (an LDS WView: one block row
+// of the tile layout with nb = blocks per step).  Decode mapping: lane =
+// 8 rows x 8 consecutive 8-element groups, so each store instruction writes
+// eight 256-byte row segments (f32; 128 bytes for halves), and the LDS reads
+// of a wave touch 8 rows x at most 2 chunks (no more than 2-way bank
+// conflicts).  Needs k % 256 == 0.
+template <int TYPE, typename OUT>
+__global__ __launch_bounds__(256) void dequant_tile_kernel(WView w, int64_t n, int64_t k, OUT *__restrict__ dst) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  constexpr int BPW = dq_blocks<TYPE>();
+  __shared__ uint4 lds[dq_lds_bytes<TYPE>() / 16];
+  const int tid = threadIdx.x;
+  const int64_t t = blockIdx.y;
+  const int64_t step = blockIdx.x;
+  const int64_t b0 = step * BPW;
+  WView lv;
+  lv.base = reinterpret_cast<const uint8_t *>(lds);
+  lv.nb = BPW;
+  int off = 0;
+#pragma unroll
+  for (int f = 0; f < ti.nf; ++f) {
+    const int bytes = kRowTile * ti.f[f].size * BPW;  // a multiple of 128
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(w.base + w.plane[f] + (t * w.nb + b0) * kRowTile * ti.f[f].size);
+    u32x4 *ldst = reinterpret_cast<u32x4 *>(lds) + off / 16;
+    for (int i = tid; i < bytes / 16; i += 256) ldst[i] = __builtin_nontemporal_load(&src[i]);
+    lv.plane[f] = off;
+    off += bytes;
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int r8 = lane >> 3, g8 = lane & 7;
+#pragma unroll 2
+  for (int it = 0; it < 8; ++it) {
+    const int pair = wave * 8 + it;  // (row octet, group octet) of the 8 x 4 in the tile step
+    const int row = 8 * (pair >> 2) + r8;
+    const int e = 64 * (pair & 3) + 8 * g8;  // element within the 256-element step
+    float v[8];
+    decode8<TYPE>(lv, 0, row, e / ti.bs, e % ti.bs, v);
+    const int64_t grow = t * kRowTile + row;
+    if (grow < n) store8<OUT>(dst + grow * k + step * 256 + e, v);
+  }
+}
+
 hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
                           hipStream_t stream) {
   const int64_t total = n * (k >> 3);
   if (total == 0) return hipSuccess;
+  if (k % 256 == 0) {
+    const dim3 grid((unsigned)(k / 256), (unsigned)((n + kRowTile - 1) / kRowTile));
+    bool ok = dispatch_type(type, [&]<int T>() {
+      if (dst_type == F32)
+        hipLaunchKernelGGL((dequant_tile_kernel<T, float>), grid, dim3(256), 0, stream, w, n, k,
+                           static_cast<float *>(dst));
+      else if (dst_type == BF16)
+        hipLaunchKernelGGL((dequant_tile_kernel<T, __bf16>), grid, dim3(256), 0, stream, w, n, k,
+                           static_cast<__bf16 *>(dst));
+      else
+        hipLaunchKernelGGL((dequant_tile_kernel<T, _Float16>), grid, dim3(256), 0, stream, w, n, k,
+                           static_cast<_Float16 *>(dst));
+    });
+    if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const int threads = 256;
   const int64_t want = (total + threads - 1) / threads;
   const int blocks = (int)(want < 262144 ? want : 262144);

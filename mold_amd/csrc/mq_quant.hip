@@ -4,11 +4,16 @@
 // crates/mold-inference/src/flux/lora.rs:849 (LoRA re-quantize)).
 //
 // The block contents follow ggml's reference quantizers (quantize_row_*_ref,
-// make_qx_quants, make_q3_quants, make_qkx2_quants), the algorithm candle's
-// k_quants port mirrors.  To produce byte-identical blocks the arithmetic is
-// performed in the same order with IEEE single-precision operations: FMA
-// contraction is disabled in this file, divisions and square roots are the
-// correctly rounded ones, and nearest_int() uses the same 1.5*2^23 magic add.
+// make_qx_quants, make_q3_quants, make_qkx2_quants; ggml, MIT License,
+// Copyright (c) 2023-2024 The ggml authors).  To produce byte-identical
+// blocks the arithmetic is performed in the same order with IEEE
+// single-precision operations: FMA contraction is disabled in this file,
+// divisions and square roots are the correctly rounded ones, and
+// nearest_int() uses the same 1.5*2^23 magic add.  Byte identity is held
+// against that ggml restatement only.  Whether candle's k_quants port makes
+// the same bytes is unpinned: its source is not available here, and its
+// Q2_K/Q4_K/Q5_K from_float may use make_qkx1_quants instead of
+// make_qkx2_quants.  Q4_0/Q4_1/Q5_0/Q5_1/Q8_0 have a single formula.
 // One thread quantizes one block; raw blocks go to a staging buffer that the
 // upload path then permutes into the tiled device layout.
 #include "mq_kernels.h"

@@ -236,21 +236,66 @@ def padded_len(n: int) -> int:
     return (n + ATTN_ROWS - 1) // ATTN_ROWS * ATTN_ROWS
 
 
-def attention_bf16(q, k, v, valid: Optional[int] = None):
+# A padded row's share of softmax mass on its valid keys, 1 - n_pad exp(-lse),
+# below which the zero-key correction is not used: dividing by a share that
+# small would amplify the f32 error of lse past bf16 precision (and a share
+# that cancels to zero or below gives inf or garbage), so such rows are
+# recomputed over their valid keys alone.
+PAD_MIN_SHARE = 2.0 ** -10
+
+
+def _attention_chunked(qb, kb, vb):
+    """Attention of bf16 q, k, v [H, L, D] -> [L, H*D] bf16, head-chunked, with
+    scores, softmax and the value product in f32 (scores rounded to bf16 would
+    err by ~0.05 at |q.k| ~ 150); the right operand of every batched product is
+    made contiguous first (k^T explicitly)."""
+    import torch
+    h, l, d = qb.shape
+    out = torch.empty((l, h * d), dtype=torch.bfloat16, device=qb.device)
+    scale = 1.0 / math.sqrt(d)
+    step = max(1, min(h, (1 << 31) // max(1, l * l * 4)))
+    for h0 in range(0, h, step):
+        h1 = min(h, h0 + step)
+        kt = kb[h0:h1].transpose(1, 2).float().contiguous()
+        s = torch.matmul(qb[h0:h1].float(), kt) * scale
+        p = torch.softmax(s, dim=-1)
+        o = torch.matmul(p, vb[h0:h1].float().contiguous())
+        out.view(l, h, d)[:, h0:h1] = o.transpose(0, 1)
+    return out
+
+
+def _no_fused_kernel(err: RuntimeError) -> bool:
+    """True when PyTorch reports that no fused attention kernel serves the device
+    or shape (as opposed to a failure such as running out of memory)."""
+    msg = str(err).lower()
+    if "out of memory" in msg:
+        return False
+    return any(s in msg for s in ("no available kernel", "not supported", "not implemented", "no kernel image",
+                                  "invalid device function", "not compiled"))
+
+
+def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
     """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] -> [valid, H*D] bf16.
 
-    Runs PyTorch's fused attention in bf16 (f32 softmax accumulation inside).
-    `valid` < L marks rows valid .. L-1 as padding whose k and v rows are zero:
-    the fused kernels run much faster at lengths that are multiples of 256
-    (1.0 vs 2.0 ms at 24 x 7168 vs 7145 tokens on an MI355X), and zero keys are
-    removed exactly afterwards.  Each of the n_pad zero keys adds exp(0) = 1 to
-    a row's softmax denominator Z and nothing to its numerator, so with the
-    log-sum-exp the kernel returns, out = out_pad / (1 - n_pad exp(-lse)).
-    Where neither fused kernel exists for the device, it falls back to
-    head-chunked bf16 products with f32 softmax on the valid rows; the right
-    operand of every batched product is made contiguous first (k^T explicitly),
-    the form that is safe for bf16 batched GEMMs on this platform.  The backend
-    used is recorded in ATTENTION_BACKEND."""
+    Runs PyTorch's fused attention in bf16 (f32 softmax accumulation inside; on
+    ROCm that is AOTriton's `attn_fwd` kernel).  `valid` < L marks rows
+    valid .. L-1 as padding whose k and v rows are zero: the fused kernels run
+    much faster at lengths that are multiples of 256 (1.0 vs 2.0 ms at
+    24 x 7168 vs 7145 tokens on an MI355X).  Each of the n_pad zero keys adds
+    exp(0) = 1 to a row's softmax denominator Z and nothing to its numerator, so
+    with the log-sum-exp the kernel returns, out = out_pad / s with
+    s = 1 - n_pad exp(-lse), the row's share of mass on its valid keys.  That
+    division only rescales the bf16 out_pad; its error is that of s, which stays
+    far below bf16 precision while s >= PAD_MIN_SHARE.  Rows under that share
+    (every valid score below about -10) are recomputed exactly over the valid
+    keys: with `guard` None this call finds them (one host synchronization) and
+    recomputes their heads; with `guard`, a 0-dim f32 device tensor, it only
+    raises guard to the largest 1 - s seen, and the caller checks it once
+    (FluxStep.forward reruns the step unpadded if any row fell under the share).
+
+    Where no fused kernel serves the device, it falls back to the exact
+    head-chunked path on the valid rows (any other error propagates).  The
+    backend used is recorded in ATTENTION_BACKEND."""
     import torch
     from torch.nn.attention import SDPBackend, sdpa_kernel
     h, l, d = q.shape
@@ -261,10 +306,19 @@ def attention_bf16(q, k, v, valid: Optional[int] = None):
             if valid < l:
                 out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
                                                                                   True)[:2]
-                fac = 1.0 / (1.0 - (l - valid) * torch.exp(-lse[0, :, :valid]))  # [h, valid] f32
+                pad_share = (l - valid) * torch.exp(-lse[0, :, :valid])  # [h, valid] f32, 1 - s
                 # one pass: correct in f32, round to bf16, write the [valid, h, d] layout
                 res = torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device)
-                torch.mul(out[0, :, :valid].transpose(0, 1), fac.transpose(0, 1)[..., None], out=res)
+                torch.mul(out[0, :, :valid].transpose(0, 1), (1.0 / (1.0 - pad_share)).transpose(0, 1)[..., None],
+                          out=res)
+                if guard is not None:
+                    torch.maximum(guard, pad_share.amax(), out=guard)
+                else:
+                    bad = (pad_share > 1.0 - PAD_MIN_SHARE).any(dim=1)
+                    if bool(bad.any()):
+                        heads = bad.nonzero().flatten()
+                        exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid])
+                        res[:, heads] = exact.view(valid, heads.numel(), d)
                 ATTENTION_BACKEND["name"] = "fused"
                 return res.reshape(valid, h * d)
             else:
@@ -272,21 +326,11 @@ def attention_bf16(q, k, v, valid: Optional[int] = None):
                     o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
             ATTENTION_BACKEND["name"] = "fused"
             return o.transpose(0, 1).reshape(valid, h * d)
-        except RuntimeError:
+        except RuntimeError as err:
+            if not _no_fused_kernel(err):
+                raise
             ATTENTION_BACKEND["name"] = "chunked"
-    qb, kb, vb = qb[:, :valid], kb[:, :valid], vb[:, :valid]
-    l = valid
-    out = torch.empty((l, h * d), dtype=torch.bfloat16, device=q.device)
-    scale = 1.0 / math.sqrt(d)
-    step = max(1, min(h, (1 << 31) // max(1, l * l * 4)))
-    for h0 in range(0, h, step):
-        h1 = min(h, h0 + step)
-        kt = kb[h0:h1].transpose(1, 2).contiguous()
-        s = torch.matmul(qb[h0:h1], kt).float() * scale
-        p = torch.softmax(s, dim=-1).to(torch.bfloat16)
-        o = torch.matmul(p, vb[h0:h1])
-        out.view(l, h, d)[:, h0:h1] = o.transpose(0, 1)
-    return out
+    return _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid])
 
 
 def attention_f32(q, k, v):
@@ -295,6 +339,29 @@ def attention_f32(q, k, v):
     h, l, d = q.shape
     o = torch.nn.functional.scaled_dot_product_attention(q[None], k[None], v[None])
     return o[0].transpose(0, 1).reshape(l, h * d)
+
+
+def run_guarded(step, fwd, *args):
+    """Run a step forward with padded attention under one guard: afterwards one
+    host synchronization reads the largest pad share of any padded row, and if
+    some row's valid-key share fell below PAD_MIN_SHARE the step reruns with
+    unpadded attention buffers (exact, slower)."""
+    import torch
+    x = args[0]
+    use = x.is_cuda and step.attn is attention_bf16 and step.pad_attention
+    step._guard = torch.zeros((), dtype=torch.float32, device=x.device) if use else None
+    try:
+        out = fwd(*args)
+        if use and float(step._guard) > 1.0 - PAD_MIN_SHARE:
+            step._guard = None
+            step.pad_attention = False
+            try:
+                out = fwd(*args)
+            finally:
+                step.pad_attention = True
+    finally:
+        step._guard = None
+    return out
 
 
 class FluxStep:
@@ -314,6 +381,8 @@ class FluxStep:
         self.gated_epilogue = True
         # fused path: projections that feed only the fused passes (qkv, linear1) are written in bf16
         self.bf16_projections = True
+        self.pad_attention = True
+        self._guard = None
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused) for the modulate and the
@@ -354,15 +423,20 @@ class FluxStep:
     def _attn_padded(self, q, k, v, valid):
         """Attention over the fused path's padded joint buffers (rows >= valid zero)."""
         if self.attn is attention_bf16:
-            return attention_bf16(q, k, v, valid)
+            return attention_bf16(q, k, v, valid, guard=self._guard)
         return self.attn(q[:, :valid], k[:, :valid], v[:, :valid])
+
+    def _joint_len(self, total: int) -> int:
+        """Rows of the joint attention buffers: padded to a multiple of 256 unless
+        a rerun for ill-conditioned padded rows turned padding off."""
+        return padded_len(total) if self.pad_attention else total
 
     def _heads_fused(self, segments, cos, sin):
         """q, k, v bf16 [H, L, D] of the joint sequence from (qkv f32 [L_seg, >= 3h],
         query-norm name, key-norm name) segments in sequence order."""
         from .fused import new_heads, qk_norm_rope
         total = sum(y.shape[0] for y, _, _ in segments)
-        q, k, v = new_heads(self.cfg.num_heads, padded_len(total), segments[0][0].device, valid=total)
+        q, k, v = new_heads(self.cfg.num_heads, self._joint_len(total), segments[0][0].device, valid=total)
         off = 0
         for y, qn, kn in segments:
             n = y.shape[0]
@@ -411,7 +485,7 @@ class FluxStep:
         bf16 = torch.bfloat16 if self.bf16_projections else torch.float32  # qkv feeds only the fused pass
         lt, H = txt.shape[0], self.cfg.num_heads
         total = lt + img.shape[0]
-        q, k, v = new_heads(H, padded_len(total), img.device, valid=total)
+        q, k, v = new_heads(H, self._joint_len(total), img.device, valid=total)
         main = torch.cuda.current_stream(img.device)
         aux = aux_stream(img.device)
         aux.wait_stream(main)
@@ -496,6 +570,9 @@ class FluxStep:
         """img [L_img, in_channels], txt [L_txt, context_in_dim], y [1, vec_in_dim],
         t and guidance [1]; ids [L, 3] f32.  Returns [L_img, in_channels] f32.
         `blocks` = (double, single) limits the number of blocks run (host leg)."""
+        return run_guarded(self, self._forward, img, img_ids, txt, txt_ids, t, y, guidance, blocks)
+
+    def _forward(self, img, img_ids, txt, txt_ids, t, y, guidance, blocks):
         import torch
         nd = self.cfg.depth if blocks is None else blocks[0]
         ns = self.cfg.depth_single_blocks if blocks is None else blocks[1]

@@ -55,7 +55,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
-from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, padded_len, silu
+from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, padded_len, run_guarded, silu
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
 MAX_PERIOD = 10000.0
@@ -232,6 +232,8 @@ class QwenImageStep:
         self.gated_epilogue = True
         # fused path: the qkv projections, which feed only the fused pass, are written in bf16
         self.bf16_projections = True
+        self.pad_attention = True
+        self._guard = None
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused): on the GPU with bf16 GEMM inputs."""
@@ -298,7 +300,8 @@ class QwenImageStep:
         total = lt + img.shape[0]
         if fused:
             from .fused import new_heads
-            heads = new_heads(self.cfg.num_attention_heads, padded_len(total), img.device, valid=total)
+            heads = new_heads(self.cfg.num_attention_heads, padded_len(total) if self.pad_attention else total,
+                              img.device, valid=total)
         if aux is None:
             tqkv = self._txt_qkv(p, txt, t_mod, txt_cos, txt_sin, heads)
         else:
@@ -326,7 +329,7 @@ class QwenImageStep:
         if aux is not None:
             main.wait_stream(aux)
         if fused and self.attn is attention_bf16:
-            a = attention_bf16(*heads, valid=total)
+            a = attention_bf16(*heads, valid=total, guard=self._guard)
         elif fused:
             a = self.attn(*(t[:, :total] for t in heads))
         else:
@@ -383,6 +386,9 @@ class QwenImageStep:
         """img [H/2*W/2, 64] packed latents, txt [L_txt, joint_attention_dim], t [1];
         grid = (H/2, W/2) in patches.  Returns [L_img, 64] f32.  `blocks` limits the
         number of blocks run (host leg)."""
+        return run_guarded(self, self._forward, img, txt, t, grid, blocks)
+
+    def _forward(self, img, txt, t, grid, blocks):
         cfg = self.cfg
         nb = cfg.num_layers if blocks is None else blocks
         rope = rope_tables(cfg, 1, grid[0], grid[1], txt.shape[0], img.device)

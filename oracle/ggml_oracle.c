@@ -4,6 +4,10 @@
  * TEST INFRASTRUCTURE ONLY (see ggml_oracle.h).  Only tests/, smoke() and the
  * cpu_baseline leg of bench.py may load this library.
  *
+ * The quantizer and dot-product routines restate ggml's (ggml-quants.c,
+ * MIT License, Copyright (c) 2023-2024 The ggml authors) step by step, since
+ * byte-identical blocks need the same IEEE operations in the same order.
+ *
  * Source of each algorithm.  candle-core-mold 0.9.10 (pinned at
  * /root/reference/Cargo.lock:507-535; not vendored, crate source absent from
  * this container) ports ggml's k_quants/ggml-quants C code.  Everything here is
@@ -12,8 +16,12 @@
  *   dequantize_row_* ......... ggml-quants.c  (candle: k_quants.rs `to_float`)
  *   quantize_row_*_ref ....... ggml-quants.c  (llama-quantize without imatrix)
  *   vec_dot_*_q8_* ........... ggml-quants.c generic paths (candle: `vec_dot_unopt`)
- *   Q8_1 / Q8_K activations .. candle k_quants.rs `from_float` (round-half-away,
- *                              Q8_K scale -128/max; ggml differs in last bits)
+ *   Q8_1 / Q8_K activations .. candle k_quants.rs `from_float` as recalled
+ *                              (round-half-away, Q8_K scale -128/max; ggml
+ *                              differs in last bits).  PARITY UNPINNED: no
+ *                              candle source or vectors exist here, so tests
+ *                              report agreement with it but assert only
+ *                              convention-independent bounds.
  *   matmul ................... candle quantized/mod.rs `matmul_t`: quantize each
  *                              activation row, then vec_dot per output column.
  * Call sites in the reference that reach these: QTensor::dequantize at

@@ -39,40 +39,60 @@ def build() -> str:
     return _LIB_PATH
 
 
+_NATIVE_PATH = os.path.join(_HERE, "liboracle_native.so")
+_native = None
+
+
+def native_lib() -> ctypes.CDLL:
+    """The same oracle compiled on this host with -march=native (the CPU
+    baseline's build: the portable liboracle.so targets x86-64-v2 so that it
+    runs on any box).  Rebuilt on first use in each process, with the
+    committed Makefile, so it always matches the CPU it runs on."""
+    global _native
+    if _native is None:
+        subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle_native.so"], check=True)
+        _native = _bind(ctypes.CDLL(_NATIVE_PATH))
+    return _native
+
+
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(_LIB_PATH):
             raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run `make -C oracle`)")
-        L = ctypes.CDLL(_LIB_PATH)
-        vp, i64, c_int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
-        L.orc_fp32_to_fp16.restype = ctypes.c_uint16
-        L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
-        L.orc_fp16_to_fp32.restype = ctypes.c_float
-        L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
-        L.orc_fp32_to_bf16.restype = ctypes.c_uint16
-        L.orc_fp32_to_bf16.argtypes = [ctypes.c_float]
-        L.orc_block_size.restype = c_int
-        L.orc_block_size.argtypes = [c_int]
-        L.orc_type_size.restype = c_int
-        L.orc_type_size.argtypes = [c_int]
-        L.orc_dequantize_row.restype = c_int
-        L.orc_dequantize_row.argtypes = [c_int, vp, vp, i64]
-        L.orc_quantize_row.restype = c_int
-        L.orc_quantize_row.argtypes = [c_int, vp, vp, i64]
-        for nm in ("orc_quantize_row_q8_0", "orc_quantize_row_q8_1", "orc_quantize_row_q8_K"):
-            getattr(L, nm).restype = None
-            getattr(L, nm).argtypes = [vp, vp, i64]
-        L.orc_vec_dot_type.restype = c_int
-        L.orc_vec_dot_type.argtypes = [c_int]
-        L.orc_vec_dot.restype = ctypes.c_float
-        L.orc_vec_dot.argtypes = [c_int, i64, vp, vp]
-        L.orc_matmul_candle.restype = c_int
-        L.orc_matmul_candle.argtypes = [c_int, i64, i64, i64, vp, vp, vp, c_int]
-        L.orc_matmul_f64.restype = c_int
-        L.orc_matmul_f64.argtypes = [c_int, i64, i64, i64, vp, vp, vp]
-        _lib = L
+        _lib = _bind(ctypes.CDLL(_LIB_PATH))
     return _lib
+
+
+def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
+    """Declare the C signatures on a loaded oracle library."""
+    vp, i64, c_int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+    L.orc_fp32_to_fp16.restype = ctypes.c_uint16
+    L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
+    L.orc_fp16_to_fp32.restype = ctypes.c_float
+    L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+    L.orc_fp32_to_bf16.restype = ctypes.c_uint16
+    L.orc_fp32_to_bf16.argtypes = [ctypes.c_float]
+    L.orc_block_size.restype = c_int
+    L.orc_block_size.argtypes = [c_int]
+    L.orc_type_size.restype = c_int
+    L.orc_type_size.argtypes = [c_int]
+    L.orc_dequantize_row.restype = c_int
+    L.orc_dequantize_row.argtypes = [c_int, vp, vp, i64]
+    L.orc_quantize_row.restype = c_int
+    L.orc_quantize_row.argtypes = [c_int, vp, vp, i64]
+    for nm in ("orc_quantize_row_q8_0", "orc_quantize_row_q8_1", "orc_quantize_row_q8_K"):
+        getattr(L, nm).restype = None
+        getattr(L, nm).argtypes = [vp, vp, i64]
+    L.orc_vec_dot_type.restype = c_int
+    L.orc_vec_dot_type.argtypes = [c_int]
+    L.orc_vec_dot.restype = ctypes.c_float
+    L.orc_vec_dot.argtypes = [c_int, i64, vp, vp]
+    L.orc_matmul_candle.restype = c_int
+    L.orc_matmul_candle.argtypes = [c_int, i64, i64, i64, vp, vp, vp, c_int]
+    L.orc_matmul_f64.restype = c_int
+    L.orc_matmul_f64.argtypes = [c_int, i64, i64, i64, vp, vp, vp]
+    return L
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -135,14 +155,17 @@ def vec_dot(t: int, k: int, w_row: np.ndarray, act_row: np.ndarray) -> float:
     return float(lib().orc_vec_dot(t, k, _ptr(w_row), _ptr(act_row)))
 
 
-def matmul_candle(t: int, x: np.ndarray, w_blocks: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
-    """candle CPU QMatMul: quantized activations x integer block dots."""
+def matmul_candle(t: int, x: np.ndarray, w_blocks: np.ndarray, n: int, k: int, nthreads: int = 0,
+                  native: bool = False) -> np.ndarray:
+    """candle CPU QMatMul: quantized activations x integer block dots
+    (`native`: the -march=native build of the same code)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     m = x.shape[0]
     assert x.shape == (m, k)
     w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
     y = np.empty((m, n), dtype=np.float32)
-    rc = lib().orc_matmul_candle(t, m, n, k, _ptr(x), _ptr(w_blocks), _ptr(y), nthreads)
+    L = native_lib() if native else lib()
+    rc = L.orc_matmul_candle(t, m, n, k, _ptr(x), _ptr(w_blocks), _ptr(y), nthreads)
     if rc != 0:
         raise ValueError(f"matmul_candle failed rc={rc}")
     return y

@@ -128,6 +128,79 @@ def test_padded_attention_matches_reference(valid, padded):
     assert err < 5e-3, err
 
 
+def _anti_aligned(valid, padded, bad_heads, H=4, D=128, seed=7):
+    """q, k, v [H, padded, D] bf16 whose heads in `bad_heads` have every valid score
+    q.k/sqrt(D) <= -10 (q anti-aligned with all keys), so the zero pad keys hold
+    nearly all of those rows' softmax mass."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v = (torch.randn((H, padded, D), device="cuda", generator=g) for _ in range(3))
+    u = torch.randn(D, device="cuda", generator=g)
+    u = u / u.norm()
+    for h in bad_heads:
+        k[h] = 12.0 * u + 0.05 * k[h]
+        q[h] = -12.0 * u + 0.05 * q[h]
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    k[:, valid:] = 0
+    v[:, valid:] = 0
+    return q, k, v
+
+
+def _attn_ref(q, k, v, valid):
+    H, _, D = q.shape
+    qf, kf, vf = (t[:, :valid].double().cpu() for t in (q, k, v))      # f64 on the host
+    s = qf @ kf.transpose(1, 2).contiguous() / np.sqrt(D)
+    return (torch.softmax(s, dim=-1) @ vf).transpose(0, 1).reshape(valid, H * D), s
+
+
+def test_padded_attention_ill_conditioned_rows_recomputed():
+    """Heads whose valid scores are all <= -10: the zero-key correction would divide by a
+    valid-key share near 0, so those heads are recomputed over the valid keys."""
+    from mold_amd.flux import attention_bf16
+    valid, padded, bad = 700, 768, [1, 3]
+    print(f"[case] anti-aligned padded attention valid={valid} padded={padded} bad heads={bad}", flush=True)
+    q, k, v = _anti_aligned(valid, padded, bad)
+    ref, s = _attn_ref(q, k, v, valid)
+    assert float(s[bad].max()) <= -10.0
+    out = attention_bf16(q, k, v, valid)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all().item()
+    H, D = q.shape[0], q.shape[2]
+    for h in range(H):
+        o, r = out.view(valid, H, D)[:, h].double().cpu(), ref.view(valid, H, D)[:, h]
+        err = ((o - r).norm() / r.norm()).item()
+        assert err < 5e-3, (h, err)
+
+
+def test_padded_attention_guard_and_step_rerun():
+    """With a guard tensor the call only records the largest pad share; run_guarded reads
+    it once and reruns the forward unpadded, which is then exact."""
+    from mold_amd.flux import PAD_MIN_SHARE, attention_bf16, run_guarded
+    valid, padded = 700, 768
+    q, k, v = _anti_aligned(valid, padded, [0, 1, 2, 3])
+    ref, _ = _attn_ref(q, k, v, valid)
+
+    class Step:
+        attn = staticmethod(attention_bf16)
+        pad_attention = True
+        _guard = None
+        calls = []
+
+        def fwd(self, x):
+            self.calls.append(self.pad_attention)
+            if self.pad_attention:
+                return attention_bf16(q, k, v, valid, guard=self._guard)
+            return attention_bf16(q[:, :valid], k[:, :valid], v[:, :valid])
+
+    st = Step()
+    guard = torch.zeros((), device="cuda")
+    attention_bf16(q, k, v, valid, guard=guard)
+    assert float(guard) > 1.0 - PAD_MIN_SHARE
+    out = run_guarded(st, st.fwd, q)
+    assert st.calls == [True, False] and st.pad_attention and st._guard is None
+    err = ((out.double().cpu() - ref).norm() / ref.norm()).item()
+    assert err < 5e-3, err
+
+
 def test_glue_errors_are_reported():
     mold_amd.load()
     y = torch.zeros((4, 3 * 128), device="cuda")
