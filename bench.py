@@ -34,6 +34,8 @@ Also on the same JSON line:
     rate;
   * "dense_bf16_ceiling": torch's bf16 linear (hipBLASLt) at the headline shape
     with a dense bf16 weight, the achievable-MFMA reference;
+  * "encoder_decode": T5-XXL encoder linears at M=512 and LLM-decode M=1
+    GEMVs at K=4096 / N=10240 (the text-encoder and prompt-expansion shapes);
   * "upload": GGUF file -> HBM rate of mq_gguf_load_tensor (pinned,
     double-buffered) over a 300 MB file just written (so read from the page
     cache: PCIe and the pipeline, not the disk), and of the host-buffer upload;
@@ -298,6 +300,66 @@ def bench_upload(dev, args):
             "host_buffer_gbs": round(count * nbytes / dt_host / 1e9, 2), "readback_identical": bool(ok),
             "what": "mq_gguf_load_tensor over a freshly written file (page cache: PCIe + pipeline, not disk), "
                     "pinned 16 MiB chunks double-buffered; host_buffer = mq_qtensor_upload from pageable numpy"}
+
+
+def bench_encoder_decode(dev, args):
+    """Next-row shapes behind the same boundary: T5-XXL encoder linears at M=512
+    (crates/mold-inference/src/encoders/t5_gguf.rs:243-279) and LLM-expand M=1
+    decode GEMVs at K=4096 / N=10240 (crates/mold-inference/src/expand.rs:200-203),
+    the decode ones rotating through > 256 MB of weight copies in a HIP graph."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    enc = []
+    m = 512
+    g = torch.Generator(device="cuda").manual_seed(70)
+    for tname in ("Q8_0", "Q5_K"):
+        for label, (n, k) in (("attn_q", (4096, 4096)), ("ffn_up", (10240, 4096)), ("ffn_down", (4096, 10240))):
+            mm = mold_amd.QMatMul(make_weight(dev, GgmlDType[tname], n, k, seed=71))
+            x = torch.randn((m, k), device="cuda", generator=g)
+            y = torch.empty((m, n), device="cuda")
+            _, ms = timed(lambda: mm.forward(x, out=y), max(20, args.steps // 4), 3, prewarm_s=0.05)
+            fl = 2.0 * m * n * k
+            enc.append({"weight": tname, "linear": label, "m": m, "n": n, "k": k, "us": round(ms * 1e3, 2),
+                        "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                        "frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+            log(f"  T5 {tname} {label} m={m}: {ms*1e3:.1f} us {enc[-1]['tflops']} TFLOP/s")
+            del mm
+    dec = []
+    for tname in ("Q8_0", "Q6_K", "Q5_K", "Q4_K", "Q4_0"):
+        for n, k in ((4096, 4096), (10240, 4096), (4096, 10240)):
+            t = GgmlDType[tname]
+            first = make_weight(dev, t, n, k, seed=80)
+            wbytes = first.storage_size_in_bytes()
+            copies = max(2, -(-(300 << 20) // wbytes))
+            mms = [mold_amd.QMatMul(first)] + [mold_amd.QMatMul(make_weight(dev, t, n, k, seed=81 + i))
+                                               for i in range(copies - 1)]
+            x = torch.randn((1, k), device="cuda", generator=g)
+            y = torch.empty((1, n), device="cuda")
+            cap = torch.cuda.Stream()
+
+            def run():
+                for mm in mms:
+                    mm.forward(x, out=y)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(cap):
+                run()              # sizes the capture stream's workspace (K-split partials)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=cap):
+                run()
+            _, ms = timed(graph.replay, max(10, args.steps // 10), 2, prewarm_s=0.05)
+            ms /= copies
+            nbytes = wbytes + 4 * k + 4 * n
+            dec.append({"weight": tname, "m": 1, "n": n, "k": k, "us": round(ms * 1e3, 3), "bytes": nbytes,
+                        "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+            log(f"  decode {tname} {k}->{n}: {ms*1e3:.2f} us {dec[-1]['gbs']} GB/s")
+            del graph, mms, first
+            torch.cuda.empty_cache()
+    return {"t5_encoder_m512": enc, "decode_gemv_m1": dec,
+            "what": "T5-XXL encoder linears (f32 x staged to bf16 + fused GEMM) and LLM-decode M=1 GEMVs "
+                    "(f32 x; Q4_K takes the Q8_K integer-dot GEMV, other types the f32-FMA GEMV)"}
 
 
 def bench_gemv(dev, args):
@@ -612,7 +674,8 @@ def main():
     ap.add_argument("--flux-only", action="store_true")
     ap.add_argument("--no-qwen", action="store_true")
     ap.add_argument("--qwen-only", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip configs 1/3, dequant, ceiling and upload legs")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs 1/3, dequant, ceiling, upload, encoder legs")
+    ap.add_argument("--encoder-only", action="store_true")
     ap.add_argument("--pmc-pass", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -632,6 +695,9 @@ def main():
         flux, _, _ = bench_flux(dev, args)
         print(json.dumps({"flux_step": flux}), flush=True)
         return
+    if args.encoder_only:
+        print(json.dumps({"encoder_decode": bench_encoder_decode(dev, args)}), flush=True)
+        return
     if args.qwen_only:
         qwen, _, _ = bench_qwen(dev, args)
         print(json.dumps({"qwen_step": qwen}), flush=True)
@@ -646,6 +712,7 @@ def main():
         extra["dequant"] = bench_dequant(dev, args)
         extra["dense_bf16_ceiling"] = bench_dense_ceiling(args)
         extra["upload"] = bench_upload(dev, args)
+        extra["encoder_decode"] = bench_encoder_decode(dev, args)
         torch.cuda.empty_cache()
         for key, v in extra.items():
             log(f"{key}: {json.dumps(v)[:300]}")
