@@ -295,11 +295,28 @@ def bench_upload(dev, args):
     qts = [mold_amd.QTensor.from_blocks(dev, t, (n, k), r) for r in raw]
     dt_host = time.perf_counter() - t0
     del qts
+    # FP8 E4M3 -> Q8_0 on the device (the FP8 checkpoint cache producer's quantize step)
+    import ctypes
+    import torch
+    from mold_amd import _lib
+    fn, fk = 21504, 3072
+    src = torch.randint(0, 126, (fn, fk), dtype=torch.uint8, device="cuda")
+    for _ in range(2):
+        h = ctypes.c_void_p()
+        t0 = time.perf_counter()
+        rc = _lib.load().mq_quantize_fp8(dev.handle, int(GgmlDType.Q8_0), fn, fk, src.data_ptr(), fk,
+                                         ctypes.c_float(1.0), None, ctypes.byref(h))
+        dt_fp8 = time.perf_counter() - t0
+        assert rc == 0
+        mold_amd.QTensor(dev, h).free()
     return {"bytes": count * nbytes, "tensors": count,
+            "fp8_to_q8_0_ms": round(dt_fp8 * 1e3, 3), "fp8_to_q8_0_gbs": round(fn * fk / dt_fp8 / 1e9, 1),
             "gguf_file_gbs": round(count * nbytes / dt_file / 1e9, 2),
             "host_buffer_gbs": round(count * nbytes / dt_host / 1e9, 2), "readback_identical": bool(ok),
             "what": "mq_gguf_load_tensor over a freshly written file (page cache: PCIe + pipeline, not disk), "
-                    "pinned 16 MiB chunks double-buffered; host_buffer = mq_qtensor_upload from pageable numpy"}
+                    "pinned 16 MiB chunks double-buffered; host_buffer = mq_qtensor_upload from pageable numpy; "
+                    "fp8_to_q8_0: mq_quantize_fp8 of a device-resident FP8 E4M3 [21504, 3072] to Q8_0 including the "
+                    "repack and the synchronization (GB/s of FP8 input)"}
 
 
 def bench_encoder_decode(dev, args):

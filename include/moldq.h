@@ -116,6 +116,15 @@ int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
  * blocks are in place (through the context's upload staging buffer). */
 int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld,
                 void *stream, mq_qtensor **out);
+/* Same from FP8 E4M3 weights already on the device: src[n, ld] bytes in the
+ * OCP "E4M3FN" encoding (safetensors F8_E4M3, torch.float8_e4m3fn), each
+ * decoded exactly to f32 and multiplied by `scale` (1 for mold's cache)
+ * before quantization.  The device side of mold's FP8 checkpoint -> Q8_0
+ * GGUF cache (ensure_fp8_gguf_cache, crates/mold-inference/src/flux/
+ * pipeline.rs:120-252, which loads the FP8 tensor and calls
+ * QTensor::quantize(.., Q8_0) at :212-216).  Synchronous like mq_quantize. */
+int mq_quantize_fp8(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *src, int64_t ld,
+                    float scale, void *stream, mq_qtensor **out);
 /* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
  * Synchronous. */
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes);
@@ -215,6 +224,55 @@ int mq_gguf_tensor_info(const mq_gguf *g, int64_t index, const char **name, int 
  * host buffers in turn, each copied to the device asynchronously while the
  * next is read, then repacked on the device.  Synchronous. */
 int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out);
+/* The tensor's raw bytes as stored (any type, dense F32/F16/BF16 included)
+ * into host memory; nbytes must equal the tensor's size.  What mold reads
+ * with content.tensor(&mut file, name, &Device::Cpu) when it copies tensors
+ * between GGUF files (flux/pipeline.rs:507-530). */
+int mq_gguf_read_tensor(const mq_gguf *g, int64_t index, void *dst, size_t nbytes);
+int mq_gguf_version(const mq_gguf *g);
+
+/* --- GGUF metadata (candle gguf_file::Content::metadata).  Value types are
+ *     GGUF's: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool,
+ *     8 string, 9 array, 10 u64, 11 i64, 12 f64.  An array reports type 9,
+ *     its element type and its length; elements are read by index (arrays
+ *     of arrays report their length only).  Strings are not NUL-free:
+ *     use the returned length. ------------------------------------------- */
+int64_t mq_gguf_kv_count(const mq_gguf *g);
+int64_t mq_gguf_find_kv(const mq_gguf *g, const char *key);  /* -1 if absent */
+int mq_gguf_kv_info(const mq_gguf *g, int64_t index, const char **key, int *type, int *elem_type,
+                    uint64_t *count);
+/* Integer or bool element `elem` (0 for a scalar). */
+int mq_gguf_kv_int(const mq_gguf *g, int64_t index, uint64_t elem, int64_t *out);
+/* f32 or f64 element. */
+int mq_gguf_kv_float(const mq_gguf *g, int64_t index, uint64_t elem, double *out);
+int mq_gguf_kv_str(const mq_gguf *g, int64_t index, uint64_t elem, const char **s, uint64_t *len);
+
+/* --- GGUF writer (candle gguf_file::write, used by mold for its FP8 -> Q8_0
+ *     cache at flux/pipeline.rs:240 and the embedding-patched cache at
+ *     :541).  Writes version 3, metadata in the order added, tensors in the
+ *     order added at offsets aligned to `alignment` (0 = 32; another value is
+ *     recorded as general.alignment).  finish() writes <path>.tmp.<pid> and
+ *     renames it over <path>, so a failed write leaves no partial file.
+ *     Device tensors added with add_qtensor are read back (as their GGUF
+ *     blocks) during finish and must stay alive until then. ------------- */
+typedef struct mq_gguf_writer mq_gguf_writer;
+int mq_gguf_writer_create(const char *path, uint32_t alignment, mq_gguf_writer **out);
+void mq_gguf_writer_free(mq_gguf_writer *w);
+int mq_gguf_writer_kv_scalar(mq_gguf_writer *w, const char *key, int type, const void *value);
+int mq_gguf_writer_kv_str(mq_gguf_writer *w, const char *key, const char *value);
+int mq_gguf_writer_kv_array(mq_gguf_writer *w, const char *key, int elem_type, const void *values,
+                            uint64_t count);
+int mq_gguf_writer_kv_str_array(mq_gguf_writer *w, const char *key, const char *const *values,
+                                uint64_t count);
+/* Raw tensor bytes from host memory (copied); dims in GGUF order (ne[0] is
+ * the contiguous dimension). */
+int mq_gguf_writer_add_tensor(mq_gguf_writer *w, const char *name, int dtype, int n_dims,
+                              const int64_t *dims, const void *data, size_t nbytes);
+/* A device-resident weight; n_dims = 0 writes it as [n, k] (ne = {k, n}),
+ * otherwise dims (ne[0] = k, same element count) give its stored shape. */
+int mq_gguf_writer_add_qtensor(mq_gguf_writer *w, mq_ctx *ctx, const char *name, const mq_qtensor *qt,
+                               int n_dims, const int64_t *dims);
+int mq_gguf_writer_finish(mq_gguf_writer *w);
 
 #ifdef __cplusplus
 }

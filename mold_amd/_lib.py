@@ -30,6 +30,7 @@ SIGNATURES = {
     "mq_qtensor_upload": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _pp]),
     "mq_qtensor_from_device": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _vp, _pp]),
     "mq_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _vp, _pp]),
+    "mq_quantize_fp8": (_int, [_vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float, _vp, _pp]),
     "mq_qtensor_download": (_int, [_vp, _vp, _vp, _sz]),
     "mq_qtensor_free": (None, [_vp]),
     "mq_qtensor_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
@@ -50,6 +51,25 @@ SIGNATURES = {
                                    ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint64),
                                    ctypes.POINTER(_sz)]),
     "mq_gguf_load_tensor": (_int, [_vp, _vp, _i64, _pp]),
+    "mq_gguf_read_tensor": (_int, [_vp, _i64, _vp, _sz]),
+    "mq_gguf_version": (_int, [_vp]),
+    "mq_gguf_kv_count": (_i64, [_vp]),
+    "mq_gguf_find_kv": (_i64, [_vp, ctypes.c_char_p]),
+    "mq_gguf_kv_info": (_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_int), ctypes.POINTER(_int),
+                               ctypes.POINTER(ctypes.c_uint64)]),
+    "mq_gguf_kv_int": (_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(_i64)]),
+    "mq_gguf_kv_float": (_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)]),
+    "mq_gguf_kv_str": (_int, [_vp, _i64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p),
+                              ctypes.POINTER(ctypes.c_uint64)]),
+    "mq_gguf_writer_create": (_int, [ctypes.c_char_p, ctypes.c_uint32, _pp]),
+    "mq_gguf_writer_free": (None, [_vp]),
+    "mq_gguf_writer_kv_scalar": (_int, [_vp, ctypes.c_char_p, _int, _vp]),
+    "mq_gguf_writer_kv_str": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p]),
+    "mq_gguf_writer_kv_array": (_int, [_vp, ctypes.c_char_p, _int, _vp, ctypes.c_uint64]),
+    "mq_gguf_writer_kv_str_array": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), ctypes.c_uint64]),
+    "mq_gguf_writer_add_tensor": (_int, [_vp, ctypes.c_char_p, _int, _int, ctypes.POINTER(_i64), _vp, _sz]),
+    "mq_gguf_writer_add_qtensor": (_int, [_vp, _vp, ctypes.c_char_p, _vp, _int, ctypes.POINTER(_i64)]),
+    "mq_gguf_writer_finish": (_int, [_vp]),
 }
 
 _lib = None

@@ -451,13 +451,15 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
   return MQ_OK;
 }
 
-int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld, void *stream,
-                mq_qtensor **out) {
-  if (!ctx || !out || !src) return fail(MQ_E_INVALID, "mq_quantize: NULL argument");
+// Shared by mq_quantize and mq_quantize_fp8: quantize src (f32 or FP8 E4M3
+// bytes) on `stream` into the upload staging buffer, then repack.
+static int quantize_common(mq_ctx *ctx, const char *fn, int dtype, int64_t n, int64_t k, const void *src, bool fp8,
+                           int64_t ld, float scale, void *stream, mq_qtensor **out) {
+  if (!ctx || !out || !src) return fail(MQ_E_INVALID, "%s: NULL argument", fn);
   *out = nullptr;
-  if (!is_quant(dtype)) return fail(MQ_E_INVALID, "mq_quantize: dtype %d is not a GGUF block type", dtype);
+  if (!is_quant(dtype)) return fail(MQ_E_INVALID, "%s: dtype %d is not a GGUF block type", fn, dtype);
   if (n <= 0 || k <= 0 || ld < k)
-    return fail(MQ_E_INVALID, "mq_quantize: bad shape n=%lld k=%lld ld=%lld", (long long)n, (long long)k, (long long)ld);
+    return fail(MQ_E_INVALID, "%s: bad shape n=%lld k=%lld ld=%lld", fn, (long long)n, (long long)k, (long long)ld);
   const TypeInfo ti = type_info(dtype);
   if (k % ti.bs != 0) return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", ti.name, ti.bs, (long long)k);
   DeviceGuard g(ctx->device);
@@ -466,7 +468,8 @@ int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, 
   uint8_t *st = nullptr;
   int rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;
-  hipError_t e = launch_quantize(dtype, src, ld, n, k, st, s);
+  hipError_t e = fp8 ? launch_quantize_fp8(dtype, static_cast<const uint8_t *>(src), ld, n, k, scale, st, s)
+                     : launch_quantize(dtype, static_cast<const float *>(src), ld, n, k, st, s);
   if (e != hipSuccess) return hip_fail(e, "quantize launch");
   rc = tensor_from_raw(ctx, dtype, n, k, st, s, out);
   if (rc) return rc;
@@ -477,6 +480,16 @@ int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, 
     return hip_fail(se, "quantize synchronize");
   }
   return MQ_OK;
+}
+
+int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld, void *stream,
+                mq_qtensor **out) {
+  return quantize_common(ctx, "mq_quantize", dtype, n, k, src, false, ld, 1.0f, stream, out);
+}
+
+int mq_quantize_fp8(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *src, int64_t ld, float scale,
+                    void *stream, mq_qtensor **out) {
+  return quantize_common(ctx, "mq_quantize_fp8", dtype, n, k, src, true, ld, scale, stream, out);
 }
 
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes) {

@@ -15,6 +15,9 @@ hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, boo
 // f32 [n, k] (row stride ld) -> raw GGUF blocks (n rows of k/bs blocks).
 hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, int64_t k, void *dst_raw,
                            hipStream_t stream);
+// Same from FP8 E4M3 bytes src[n, ld] (decoded exactly, times scale).
+hipError_t launch_quantize_fp8(int type, const uint8_t *src, int64_t ld, int64_t n, int64_t k, float scale,
+                               void *dst_raw, hipStream_t stream);
 hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
                           hipStream_t stream);
 // bf16 [m, k] (row stride ldx) -> f32 [m, k] contiguous, for the GEMV.

@@ -541,39 +541,68 @@ __device__ __forceinline__ void quant_block(const float *x, uint8_t *o) {
   else q_q6_K(x, o);
 }
 
-// One thread per block: copy the block's inputs to private memory, quantize
-// into a private block image, store it to the raw staging buffer.
-template <int TYPE>
-__global__ __launch_bounds__(64) void quantize_kernel(const float *__restrict__ src, int64_t ld, int64_t n,
-                                                      int64_t nb, uint8_t *__restrict__ dst) {
+// FP8 E4M3 ("fn": bias 7, no infinities, S.1111.111 is NaN) to f32, exact.
+__device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
+  const uint32_t sign = (uint32_t)(b & 0x80) << 24;
+  const uint32_t e = (b >> 3) & 0xF, m = b & 7;
+  if (e == 0xF && m == 7) return __uint_as_float(sign | 0x7FC00000u);
+  if (e == 0) {
+    const float v = (float)m * 0.001953125f;  // m / 8 * 2^-6
+    return sign ? -v : v;
+  }
+  return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+// One thread per block: copy the block's inputs to private memory (f32 as
+// given, or FP8 E4M3 decoded exactly and multiplied by `scale`), quantize into
+// a private block image, store it to the raw staging buffer.
+template <int TYPE, bool FP8>
+__global__ __launch_bounds__(64) void quantize_kernel(const void *__restrict__ src, int64_t ld, int64_t n,
+                                                      int64_t nb, float scale, uint8_t *__restrict__ dst) {
   constexpr TypeInfo ti = type_info(TYPE);
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n * nb) return;
   const int64_t row = i / nb, b = i - row * nb;
   float x[ti.bs];
-  const float *p = src + row * ld + b * ti.bs;
-  for (int j = 0; j < ti.bs; ++j) x[j] = p[j];
+  if constexpr (FP8) {
+    const uint8_t *p = static_cast<const uint8_t *>(src) + row * ld + b * ti.bs;
+    for (int j = 0; j < ti.bs; ++j) x[j] = e4m3_to_f32(p[j]) * scale;
+  } else {
+    const float *p = static_cast<const float *>(src) + row * ld + b * ti.bs;
+    for (int j = 0; j < ti.bs; ++j) x[j] = p[j];
+  }
   uint8_t o[ti.ts];
   quant_block<TYPE>(x, o);
   uint8_t *q = dst + i * ti.ts;
   for (int j = 0; j < ti.ts; ++j) q[j] = o[j];
 }
 
-}  // namespace
-
-hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, int64_t k, void *dst_raw,
-                           hipStream_t stream) {
+template <bool FP8>
+hipError_t launch_quantize_src(int type, const void *src, int64_t ld, int64_t n, int64_t k, float scale,
+                               void *dst_raw, hipStream_t stream) {
   const TypeInfo ti = type_info(type);
   const int64_t nb = k / ti.bs;
   const int64_t total = n * nb;
   if (total == 0) return hipSuccess;
   const unsigned grid = (unsigned)((total + 63) / 64);
   bool ok = dispatch_type(type, [&]<int T>() {
-    hipLaunchKernelGGL(quantize_kernel<T>, dim3(grid), dim3(64), 0, stream, src, ld, n, nb,
+    hipLaunchKernelGGL((quantize_kernel<T, FP8>), dim3(grid), dim3(64), 0, stream, src, ld, n, nb, scale,
                        static_cast<uint8_t *>(dst_raw));
   });
   if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, int64_t k, void *dst_raw,
+                           hipStream_t stream) {
+  return launch_quantize_src<false>(type, src, ld, n, k, 1.0f, dst_raw, stream);
+}
+
+hipError_t launch_quantize_fp8(int type, const uint8_t *src, int64_t ld, int64_t n, int64_t k, float scale,
+                               void *dst_raw, hipStream_t stream) {
+  return launch_quantize_src<true>(type, src, ld, n, k, scale, dst_raw, stream);
 }
 
 }  // namespace mq

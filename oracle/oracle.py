@@ -189,3 +189,17 @@ def rel_l2(a: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, dtype=np.float64)
     den = np.linalg.norm(ref.ravel())
     return float(np.linalg.norm((a - ref).ravel()) / (den if den > 0 else 1.0))
+
+
+def e4m3_to_f32(b: np.ndarray) -> np.ndarray:
+    """FP8 E4M3 ("fn": bias 7, no infinities, S.1111.111 NaN) bytes -> f32,
+    exact (the OCP 8-bit float spec; safetensors F8_E4M3).  Normal:
+    (-1)^s 2^(e-7) (1 + m/8); subnormal (e = 0): (-1)^s 2^-6 m/8."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    s = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = (s * mag).astype(np.float32)
+    out[(e == 0xF) & (m == 7)] = np.nan
+    return out

@@ -100,6 +100,6 @@ def test_gguf_rejects_garbage(tmp_path):
     good = tmp_path / "t.gguf"
     gguf.write(str(good), [("w", GgmlDType.Q8_0, (2, 32), O.quantize(O.Q8_0, np.ones((2, 32), np.float32)))])
     data = good.read_bytes()
-    (tmp_path / "trunc.gguf").write_bytes(data[:-10])
+    (tmp_path / "trunc.gguf").write_bytes(data[:-60])   # past the trailing padding, into the data
     with pytest.raises(mold_amd.MoldqError):
         gguf.Content.read(str(tmp_path / "trunc.gguf"))
