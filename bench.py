@@ -36,6 +36,8 @@ Also on the same JSON line:
     with a dense bf16 weight, the achievable-MFMA reference;
   * "encoder_decode": T5-XXL encoder linears at M=512 and LLM-decode M=1
     GEMVs at K=4096 / N=10240 (the text-encoder and prompt-expansion shapes);
+  * "lora_merge": device LoRA merge (dequantize -> rank-32 patches ->
+    re-quantize) of a single-block linear1, with the host chain on a sample;
   * "upload": GGUF file -> HBM rate of mq_gguf_load_tensor (pinned,
     double-buffered) over a 300 MB file just written (so read from the page
     cache: PCIe and the pipeline, not the disk), and of the host-buffer upload;
@@ -379,6 +381,53 @@ def bench_encoder_decode(dev, args):
                     "(f32 x; Q4_K takes the Q8_K integer-dot GEMV, other types the f32-FMA GEMV)"}
 
 
+def bench_lora(dev, args):
+    """Device LoRA merge of one FLUX single-block linear1 (Q4_K 21504x3072) with
+    rank-32 patches on Q, K, V and the MLP rows (mold's gguf_lora_var_builder,
+    crates/mold-inference/src/flux/lora.rs:748-849): dequantize -> 4 x
+    mq_lora_apply -> quantize, and the same chain on the host (oracle) over a
+    256-row sample, scaled to the whole tensor."""
+    import numpy as np
+    import torch
+    from mold_amd import GgmlDType
+    from mold_amd import lora as L
+    n, k, rank = 21504, 3072, 32
+    qt = make_weight(dev, GgmlDType.Q4_K, n, k, seed=90)
+    g = torch.Generator(device="cuda").manual_seed(91)
+    pts = []
+    for comp, size in ((0, 3072), (1, 3072), (2, 3072), (3, 12288)):
+        a = torch.randn((rank, k), device="cuda", generator=g) * 0.05
+        b = torch.randn((size, rank), device="cuda", generator=g) * 0.05
+        pts.append(L.LoraPatch(a, b, 0.5, L.LoraTarget("single_blocks.0.linear1.weight", comp, 0)))
+    L.patch_qtensor(qt, pts)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        out, applied = L.patch_qtensor(qt, pts)
+        del out
+    torch.cuda.synchronize()
+    dev_ms = (time.perf_counter() - t0) * 1e3 / reps
+    res = {"weight": "Q4_K", "n": n, "k": k, "rank": rank, "patches": applied, "device_ms": round(dev_ms, 2),
+           "what": "mq_dequantize + 4 mq_lora_apply (Q, K, V 3072 rows, MLP 12288 rows) + mq_quantize (ggml "
+                   "reference Q4_K quantizer), synchronous"}
+    if not args.no_cpu:
+        from oracle import oracle as O
+        rows = 256
+        blocks = qt.data()[: rows * O.row_bytes(O.Q4_K, k)]
+        a = pts[0].a.cpu().numpy()
+        b = pts[0].b[:rows].cpu().numpy()
+        t0 = time.perf_counter()
+        dq = O.dequantize(O.Q4_K, blocks, rows, k)
+        dq = O.lora_apply(dq, b, a, 0.5)
+        O.quantize(O.Q4_K, dq)
+        dt = time.perf_counter() - t0
+        res["cpu_ms_extrapolated"] = round(dt * 1e3 * n / rows, 1)
+        res["cpu_sample"] = f"{rows} of {n} rows, one thread (oracle dequantize + merge + reference quantize), x{n // rows}"
+    log(f"  LoRA merge: device {dev_ms:.1f} ms" + (f", CPU ~{res['cpu_ms_extrapolated']:.0f} ms" if "cpu_ms_extrapolated" in res else ""))
+    return res
+
+
 def bench_gemv(dev, args):
     import torch
     import mold_amd
@@ -713,7 +762,8 @@ def main():
         print(json.dumps({"flux_step": flux}), flush=True)
         return
     if args.encoder_only:
-        print(json.dumps({"encoder_decode": bench_encoder_decode(dev, args)}), flush=True)
+        print(json.dumps({"encoder_decode": bench_encoder_decode(dev, args), "lora_merge": bench_lora(dev, args),
+                          "upload": bench_upload(dev, args)}), flush=True)
         return
     if args.qwen_only:
         qwen, _, _ = bench_qwen(dev, args)
@@ -730,6 +780,7 @@ def main():
         extra["dense_bf16_ceiling"] = bench_dense_ceiling(args)
         extra["upload"] = bench_upload(dev, args)
         extra["encoder_decode"] = bench_encoder_decode(dev, args)
+        extra["lora_merge"] = bench_lora(dev, args)
         torch.cuda.empty_cache()
         for key, v in extra.items():
             log(f"{key}: {json.dumps(v)[:300]}")

@@ -231,6 +231,18 @@ int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor
 int mq_gguf_read_tensor(const mq_gguf *g, int64_t index, void *dst, size_t nbytes);
 int mq_gguf_version(const mq_gguf *g);
 
+/* LoRA merge step on a dense f32 matrix on the device (the dequantized
+ * weight or a row slice of it): w[rows, k] += (b[rows, rank] . a[rank, k]) *
+ * scale, in place.  Order per element: d = 0; d = fma(b[i][r], a[r][j], d)
+ * for r = 0 .. rank-1; w = w + d * scale (rounded multiply, rounded add).
+ * Between mq_dequantize and mq_quantize it replaces the CPU round trip of
+ * mold's gguf_lora_var_builder (crates/mold-inference/src/flux/lora.rs:
+ * 759-850: dequantize to CPU f32, b.matmul(a) * effective_scale, add on the
+ * target rows, QTensor::quantize_onto).  Leading dimensions in elements.
+ * Asynchronous on `stream`; allocates nothing. */
+int mq_lora_apply(float *w, int64_t ldw, int64_t rows, int64_t k, const float *b, int64_t ldb,
+                  const float *a, int64_t lda, int rank, float scale, void *stream);
+
 /* --- GGUF metadata (candle gguf_file::Content::metadata).  Value types are
  *     GGUF's: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool,
  *     8 string, 9 array, 10 u64, 11 i64, 12 f64.  An array reports type 9,

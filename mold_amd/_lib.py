@@ -30,6 +30,7 @@ SIGNATURES = {
     "mq_qtensor_upload": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _pp]),
     "mq_qtensor_from_device": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _vp, _pp]),
     "mq_quantize": (_int, [_vp, _int, _i64, _i64, _vp, _i64, _vp, _pp]),
+    "mq_lora_apply": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, ctypes.c_float, _vp]),
     "mq_quantize_fp8": (_int, [_vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float, _vp, _pp]),
     "mq_qtensor_download": (_int, [_vp, _vp, _vp, _sz]),
     "mq_qtensor_free": (None, [_vp]),

@@ -1409,3 +1409,14 @@ int orc_matmul_f64(int type, int64_t m, int64_t n, int64_t k, const float *x, co
     run_split(&proto, resolve_threads(0, n), mm_f64_worker);
     return 0;
 }
+
+void orc_lora_apply(float *w, int64_t ldw, int64_t rows, int64_t k, const float *b, int64_t ldb,
+                    const float *a, int64_t lda, int rank, float scale) {
+  for (int64_t i = 0; i < rows; ++i)
+    for (int64_t j = 0; j < k; ++j) {
+      float d = 0.f;
+      for (int r = 0; r < rank; ++r) d = fmaf(b[i * ldb + r], a[(int64_t)r * lda + j], d);
+      const float t = d * scale;
+      w[i * ldw + j] = w[i * ldw + j] + t;
+    }
+}

@@ -71,6 +71,15 @@ int orc_matmul_candle(int type, int64_t m, int64_t n, int64_t k, const float *x,
 int orc_matmul_f64(int type, int64_t m, int64_t n, int64_t k, const float *x,
                    const void *w, double *y);
 
+/* LoRA merge of mold's GGUF LoRA path (crates/mold-inference/src/flux/
+ * lora.rs:771-833: delta = (B . A) * scale, t = t + delta on a row slice), in
+ * the order the device kernel defines: per element d = 0, then
+ * d = fmaf(b[i][r], a[r][j], d) for r = 0 .. rank-1, then
+ * w[i][j] = w[i][j] + d * scale (a rounded multiply, then a rounded add).
+ * w is [rows][ldw], b is [rows][ldb], a is [rank][lda]. */
+void orc_lora_apply(float *w, int64_t ldw, int64_t rows, int64_t k, const float *b, int64_t ldb,
+                    const float *a, int64_t lda, int rank, float scale);
+
 #ifdef __cplusplus
 }
 #endif

@@ -92,6 +92,8 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.orc_matmul_candle.argtypes = [c_int, i64, i64, i64, vp, vp, vp, c_int]
     L.orc_matmul_f64.restype = c_int
     L.orc_matmul_f64.argtypes = [c_int, i64, i64, i64, vp, vp, vp]
+    L.orc_lora_apply.restype = None
+    L.orc_lora_apply.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, c_int, ctypes.c_float]
     return L
 
 
@@ -203,3 +205,16 @@ def e4m3_to_f32(b: np.ndarray) -> np.ndarray:
     out = (s * mag).astype(np.float32)
     out[(e == 0xF) & (m == 7)] = np.nan
     return out
+
+
+def lora_apply(w: np.ndarray, b: np.ndarray, a: np.ndarray, scale: float) -> np.ndarray:
+    """w + (b . a) * scale in the device kernel's order (see orc_lora_apply);
+    w [rows, k], b [rows, rank], a [rank, k], all f32.  Returns a new array."""
+    w = np.array(w, dtype=np.float32, order="C", copy=True)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    rows, k = w.shape
+    rank = b.shape[1]
+    assert b.shape == (rows, rank) and a.shape == (rank, k)
+    lib().orc_lora_apply(_ptr(w), k, rows, k, _ptr(b), rank, _ptr(a), k, rank, float(scale))
+    return w
