@@ -51,7 +51,9 @@ Also on the same JSON line:
     (60 dual-stream blocks, 6889 image + 256 text
     tokens, q/k/v Q3_K, MLP Q2_K, out-projections and modulation Q4_K), built
     by mold_amd.qwen_image, in ms per step, with a host-CPU baseline (stems,
-    block 0 and the output layer on the CPU, extrapolated x60);
+    block 0 and the output layer on the CPU, extrapolated x60), and the
+    batch-2 classifier-free-guidance forward (cond + a shorter, masked uncond
+    prompt) in ms ("cfg_batch2_ms");
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
     oracle/, timed on a bounded row sample of the headline workload on this
@@ -532,6 +534,25 @@ def bench_qwen(dev, args):
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
     assert torch.isfinite(out).all().item(), "non-finite Qwen step output"
+    # CFG batching (pipeline.rs:1866-1899): cond + uncond in one batch-2 forward,
+    # the uncond prompt 180 of 256 tokens (its padding masked out of attention)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    txt_u = torch.randn(inp["txt"].shape, device="cuda", generator=g)
+    b_args = (torch.stack([inp["img"], inp["img"]]), torch.stack([inp["txt"], txt_u]),
+              torch.cat([inp["t"], inp["t"]]), inp["grid"])
+    outb = step.forward_batched(*b_args, txt_valid=[256, 180])
+    torch.cuda.synchronize()
+    btimes = []
+    for _ in range(max(2, n // 2)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outb = step.forward_batched(*b_args, txt_valid=[256, 180])
+        torch.cuda.synchronize()
+        btimes.append((time.perf_counter() - t0) * 1e3)
+    assert torch.isfinite(outb).all().item(), "non-finite batched Qwen output"
+    bms = sorted(btimes)[len(btimes) // 2]
+    log(f"  CFG batch-2 forward {bms:.2f} ms (two batch-1 forwards: {2 * sorted(times)[len(times) // 2]:.2f} ms)")
+    del outb, b_args, txt_u
     l_img = inp["grid"][0] * inp["grid"][1]
     lin, attn = Q.step_flop(cfg, l_img, 256)
     ms = sorted(times)[len(times) // 2]
@@ -539,6 +560,7 @@ def bench_qwen(dev, args):
     res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
+           "cfg_batch2_ms": round(bms, 3), "cfg_batch2_steps_timed": len(btimes),
            "weight_bytes": params.quantized_bytes(), "attention": ATTENTION_BACKEND["name"],
            "config": f"Qwen-Image shape, 1328x1328, batch 1, {l_img} img + 256 txt tokens, 60 blocks; "
                      "q/k/v Q3_K (stacked per stream), MLP Q2_K, out-projections, modulation, stems Q4_K; "

@@ -244,11 +244,12 @@ def padded_len(n: int) -> int:
 PAD_MIN_SHARE = 2.0 ** -10
 
 
-def _attention_chunked(qb, kb, vb):
+def _attention_chunked(qb, kb, vb, drop: Optional[Tuple[int, int]] = None):
     """Attention of bf16 q, k, v [H, L, D] -> [L, H*D] bf16, head-chunked, with
     scores, softmax and the value product in f32 (scores rounded to bf16 would
     err by ~0.05 at |q.k| ~ 150); the right operand of every batched product is
-    made contiguous first (k^T explicitly)."""
+    made contiguous first (k^T explicitly).  Keys drop[0] .. drop[1]-1 are
+    masked out (score -inf)."""
     import torch
     h, l, d = qb.shape
     out = torch.empty((l, h * d), dtype=torch.bfloat16, device=qb.device)
@@ -258,6 +259,8 @@ def _attention_chunked(qb, kb, vb):
         h1 = min(h, h0 + step)
         kt = kb[h0:h1].transpose(1, 2).float().contiguous()
         s = torch.matmul(qb[h0:h1].float(), kt) * scale
+        if drop is not None and drop[1] > drop[0]:
+            s[..., drop[0]:drop[1]] = float("-inf")
         p = torch.softmax(s, dim=-1)
         o = torch.matmul(p, vb[h0:h1].float().contiguous())
         out.view(l, h, d)[:, h0:h1] = o.transpose(0, 1)
@@ -274,7 +277,7 @@ def _no_fused_kernel(err: RuntimeError) -> bool:
                                   "invalid device function", "not compiled"))
 
 
-def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
+def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optional[Tuple[int, int]] = None):
     """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] -> [valid, H*D] bf16.
 
     Runs PyTorch's fused attention in bf16 (f32 softmax accumulation inside; on
@@ -293,6 +296,10 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
     raises guard to the largest 1 - s seen, and the caller checks it once
     (FluxStep.forward reruns the step unpadded if any row fell under the share).
 
+    `drop` = (lo, hi) masks keys lo .. hi-1 (a text attention mask, e.g. the
+    padded tail of a shorter prompt in a CFG batch): their k and v rows must be
+    zero, so they are removed by the same correction (n_pad counts them too).
+
     Where no fused kernel serves the device, it falls back to the exact
     head-chunked path on the valid rows (any other error propagates).  The
     backend used is recorded in ATTENTION_BACKEND."""
@@ -301,12 +308,13 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
     h, l, d = q.shape
     valid = l if valid is None else valid
     qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
+    n_drop = 0 if drop is None else max(0, drop[1] - drop[0])
     if ATTENTION_BACKEND["name"] in (None, "fused"):
         try:
-            if valid < l:
+            if valid < l or n_drop:
                 out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
                                                                                   True)[:2]
-                pad_share = (l - valid) * torch.exp(-lse[0, :, :valid])  # [h, valid] f32, 1 - s
+                pad_share = (l - valid + n_drop) * torch.exp(-lse[0, :, :valid])  # [h, valid] f32, 1 - s
                 # one pass: correct in f32, round to bf16, write the [valid, h, d] layout
                 res = torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device)
                 torch.mul(out[0, :, :valid].transpose(0, 1), (1.0 / (1.0 - pad_share)).transpose(0, 1)[..., None],
@@ -317,7 +325,7 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
                     bad = (pad_share > 1.0 - PAD_MIN_SHARE).any(dim=1)
                     if bool(bad.any()):
                         heads = bad.nonzero().flatten()
-                        exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid])
+                        exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid], drop)
                         res[:, heads] = exact.view(valid, heads.numel(), d)
                 ATTENTION_BACKEND["name"] = "fused"
                 return res.reshape(valid, h * d)
@@ -330,7 +338,7 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None):
             if not _no_fused_kernel(err):
                 raise
             ATTENTION_BACKEND["name"] = "chunked"
-    return _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid])
+    return _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid], drop)
 
 
 def attention_f32(q, k, v):

@@ -388,6 +388,105 @@ class QwenImageStep:
         number of blocks run (host leg)."""
         return run_guarded(self, self._forward, img, txt, t, grid, blocks)
 
+    # ------------------------------------------------------------ batch (CFG)
+    def forward_batched(self, img, txt, t, grid: Tuple[int, int], txt_valid=None, blocks: Optional[int] = None):
+        """The batched forward mold runs for classifier-free guidance
+        (pipeline.rs:1866-1899 batches cond and uncond along dim 0 when
+        supports_cfg_batching(), quantized_transformer.rs:1044-1046; the forward
+        is :1048-1139 with batch B): img [B, L, 64], txt [B, L_txt, 3584], t [B],
+        `txt_valid` the number of valid (mask = 1) leading text tokens per element
+        (the encoder_attention_mask of a padded prompt; default all).  Masked text
+        keys are excluded from attention (:764-768, :804-823); masked text rows
+        still run through the text stream, as in mold.  Every linear runs once
+        over all B elements' rows (the image GEMMs at M = B*L); modulation,
+        gating and attention are per element.  GPU fused path only.  Returns
+        [B, L, 64] f32."""
+        import torch
+        B, L, _ = img.shape
+        lt = txt.shape[1]
+        if not self._fused(img.reshape(B * L, -1)):
+            raise ValueError("forward_batched runs on the GPU with bf16 GEMM inputs")
+        valid = [lt] * B if txt_valid is None else [int(v) for v in txt_valid]
+        if len(valid) != B or any(v < 1 or v > lt for v in valid):
+            raise ValueError("txt_valid needs one count in 1 .. L_txt per batch element")
+        return run_guarded(self, self._forward_batched, img, txt, t, grid, valid, blocks)
+
+    def _mod_rows(self, x, mods, j0, j1, B):
+        """Per-element modulate of x [B*Lx, h] with chunks j0 (shift), j1 (scale)
+        of each element's modulation, into one bf16 [B*Lx, h] buffer."""
+        import torch
+        from .fused import adaln_modulate
+        lx = x.shape[0] // B
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+        for b in range(B):
+            adaln_modulate(x[b * lx:(b + 1) * lx], mods[b][j0], mods[b][j1], out=out[b * lx:(b + 1) * lx])
+        return out
+
+    def _gated_rows(self, name, h, mods, j, res, B):
+        """res[b rows] += gate_b * lin(h[b rows]) per element (GEMM epilogue)."""
+        lx = res.shape[0] // B
+        for b in range(B):
+            self.p.lin[name].gated_add(h[b * lx:(b + 1) * lx], mods[b][j], res[b * lx:(b + 1) * lx])
+        return res
+
+    def block_batched(self, i, img, txt, ts, rope, B, valid):
+        import torch
+        from .fused import new_heads, qk_norm_rope
+        cfg, P = self.cfg, self.p
+        p = f"transformer_blocks.{i}."
+        img_cos, img_sin, txt_cos, txt_sin = rope
+        L, lt = img.shape[0] // B, txt.shape[0] // B
+        H = cfg.num_attention_heads
+        im = [r.chunk(6, dim=-1) for r in P.lin[p + "img_mod.1"].forward(ts)]      # M = B GEMV
+        tm = [r.chunk(6, dim=-1) for r in P.lin[p + "txt_mod.1"].forward(ts)]
+        y = P.lin[p + "attn.to_qkv"].forward(self._mod_rows(img, im, 0, 1, B), out_dtype=torch.bfloat16)
+        ty = P.lin[p + "attn.add_qkv_proj"].forward(self._mod_rows(txt, tm, 0, 1, B), out_dtype=torch.bfloat16)
+        total = lt + L
+        i_att = torch.empty((B * L, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
+        t_att = torch.empty((B * lt, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
+        for b in range(B):
+            heads = new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total)
+            qk_norm_rope(ty[b * lt:(b + 1) * lt], H, P.dense[p + "attn.norm_added_q.weight"],
+                         P.dense[p + "attn.norm_added_k.weight"], txt_cos, txt_sin, *heads, 0, cfg.norm_eps)
+            qk_norm_rope(y[b * L:(b + 1) * L], H, P.dense[p + "attn.norm_q.weight"], P.dense[p + "attn.norm_k.weight"],
+                         img_cos, img_sin, *heads, lt, cfg.norm_eps)
+            drop = None
+            if valid[b] < lt:
+                drop = (valid[b], lt)
+                heads[1][:, valid[b]:lt].zero_()
+                heads[2][:, valid[b]:lt].zero_()
+            if self.pad_attention:
+                a = attention_bf16(*heads, valid=total, guard=self._guard, drop=drop)
+            else:   # the guarded rerun: exact attention over the kept keys
+                from .flux import _attention_chunked
+                a = _attention_chunked(*(t[:, :total] for t in heads), drop)
+            t_att[b * lt:(b + 1) * lt] = a[:lt]
+            i_att[b * L:(b + 1) * L] = a[lt:]
+        txt = self._gated_rows(p + "attn.to_add_out", t_att, tm, 2, txt, B)
+        h = P.lin[p + "txt_mlp.net.0.proj"].forward(self._mod_rows(txt, tm, 3, 4, B), act=ACT_GELU_TANH,
+                                                    out_dtype=torch.bfloat16)
+        txt = self._gated_rows(p + "txt_mlp.net.2", h, tm, 5, txt, B)
+        img = self._gated_rows(p + "attn.to_out.0", i_att, im, 2, img, B)
+        h = P.lin[p + "img_mlp.net.0.proj"].forward(self._mod_rows(img, im, 3, 4, B), act=ACT_GELU_TANH,
+                                                    out_dtype=torch.bfloat16)
+        img = self._gated_rows(p + "img_mlp.net.2", h, im, 5, img, B)
+        return img, txt
+
+    def _forward_batched(self, img, txt, t, grid, valid, blocks):
+        import torch
+        cfg = self.cfg
+        B, L, c = img.shape
+        lt = txt.shape[1]
+        nb = cfg.num_layers if blocks is None else blocks
+        rope = rope_tables(cfg, 1, grid[0], grid[1], lt, img.device)
+        img_h, txt_h, temb = self.stems(img.reshape(B * L, c), txt.reshape(B * lt, -1), t)
+        ts = silu(temb)                                   # [B, h]
+        for i in range(nb):
+            img_h, txt_h = self.block_batched(i, img_h, txt_h, ts, rope, B, valid)
+        om = [r.chunk(2, dim=-1) for r in self.p.lin["norm_out.linear"].forward(ts)]   # (scale, shift)
+        x = self._mod_rows(img_h, [(o[1], o[0]) for o in om], 0, 1, B)
+        return self.p.lin["proj_out"].forward(x, out_dtype=torch.float32).reshape(B, L, -1)
+
     def _forward(self, img, txt, t, grid, blocks):
         cfg = self.cfg
         nb = cfg.num_layers if blocks is None else blocks

@@ -210,3 +210,46 @@ def test_qwen_step_tiny_matches_dequantized_reference():
     ser = Q.QwenImageStep(params, overlap=False).forward(**inp)
     torch.cuda.synchronize()
     assert torch.equal(out, ser)
+
+
+@pytest.mark.gpu
+def test_qwen_cfg_batch2_matches_two_single_forwards():
+    """Batched CFG forward (cond + uncond along dim 0, the uncond prompt shorter
+    and padded, its padding masked out of attention) against two batch-1 forwards
+    (the uncond one on its valid tokens only) and against the f64 restatement."""
+    import mold_amd
+    from oracle import oracle as O
+    cfg = Q.QwenConfig.tiny()
+    print("[qwen] tiny CFG batch-2 forward with a masked uncond prompt", flush=True)
+    dev = mold_amd.Device(0)
+    params = Q.QwenParams.random(cfg, dev, seed=11)
+    inp = Q.make_inputs(cfg, height=272, width=240, txt_len=40, device="cuda", seed=11)
+    g = torch.Generator(device="cuda").manual_seed(12)
+    txt_u = torch.randn(inp["txt"].shape, device="cuda", generator=g)
+    nv = 33
+    txt_u[nv:] = 0.0                                   # the padded tail (masked)
+    step = Q.QwenImageStep(params)
+    img2 = torch.stack([inp["img"], inp["img"]])
+    txt2 = torch.stack([inp["txt"], txt_u])
+    t2 = torch.cat([inp["t"], inp["t"]])
+    out = step.forward_batched(img2, txt2, t2, inp["grid"], txt_valid=[40, nv])
+    out_b = step.forward_batched(img2, txt2, t2, inp["grid"], txt_valid=[40, nv])
+    c0 = step.forward(inp["img"], inp["txt"], inp["t"], inp["grid"])
+    u0 = step.forward(inp["img"], txt_u[:nv].contiguous(), inp["t"], inp["grid"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_b), "batched forward is not deterministic"
+    assert out.shape == (2,) + tuple(c0.shape) and torch.isfinite(out).all().item()
+    e0, e1 = _rel(out[0].cpu().numpy(), c0.cpu().numpy()), _rel(out[1].cpu().numpy(), u0.cpu().numpy())
+    print(f"[qwen] batched vs single: cond {e0:.2e}  uncond(masked) {e1:.2e}", flush=True)
+    assert e0 <= 1e-3 and e1 <= 1e-3
+    W = {}
+    for name, l in params.lin.items():
+        qt = l.matmul.w
+        n, k = qt.shape
+        W[name] = (torch.from_numpy(O.dequantize(int(qt.dtype()), qt.data(), n, k)), l.bias.cpu())
+    D = {k_: v.float().cpu() for k_, v in params.dense.items()}
+    ref_u = reference_forward(cfg, W, D, {"img": inp["img"].cpu(), "txt": txt_u[:nv].cpu(), "t": inp["t"].cpu(),
+                                          "grid": inp["grid"]})
+    err = _rel(out[1].cpu().numpy(), ref_u.numpy())
+    print(f"[qwen] batched uncond vs f64 restatement on its valid tokens: {err:.2e}", flush=True)
+    assert err <= STEP_TOL
