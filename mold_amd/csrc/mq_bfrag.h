@@ -17,7 +17,8 @@
 //                    unit u+1 right after step G of unit u, so every weight
 //                    load has about a unit of MFMA work to land;
 //   prep()           unpacks the unit's scales into Sc once;
-//   frag<G, S>()     the bf16x8 B fragment of slice S of step G.
+//   frag<G, S>()     the bf16x8 B fragment of slice S of step G (frag<G, S,
+//                    f32x8>: the same eight weights exact in f32, for the GEMV).
 // Every weight is produced as RNE_bf16 of the exact f32 value ggml's
 // dequantize_row_* computes: each decoder uses one fma whose product is exact
 // and whose addition is the one rounding ggml performs (or is exact).
@@ -42,8 +43,13 @@ __device__ __forceinline__ uint32_t opaque(uint32_t w) {
   return w;
 }
 
-// Eight fma(byte_e(word), a, b) for the bytes of two words, as bf16.
-__device__ __forceinline__ bf16x8 fma8(uint32_t w0, uint32_t w1, float a, float b) {
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// Eight fma(byte_e(word), a, b) for the bytes of two words: the exact f32
+// weights (O = f32x8, the GEMV's), or those rounded to bf16 (O = bf16x8, the
+// MFMA B fragment).
+template <typename O = bf16x8>
+__device__ __forceinline__ O fma8(uint32_t w0, uint32_t w1, float a, float b) {
   w0 = opaque(w0);
   w1 = opaque(w1);
   float v[8];
@@ -55,9 +61,12 @@ __device__ __forceinline__ bf16x8 fma8(uint32_t w0, uint32_t w1, float a, float 
   v[5] = __builtin_fmaf(ub<1>(w1), a, b);
   v[6] = __builtin_fmaf(ub<2>(w1), a, b);
   v[7] = __builtin_fmaf(ub<3>(w1), a, b);
-  bf16x8 r;
+  O r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = (__bf16)v[i];
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (__is_same(O, f32x8)) r[i] = v[i];
+    else r[i] = (__bf16)v[i];
+  }
   return r;
 }
 
@@ -136,8 +145,8 @@ struct TK45 {
     s.m47 = ((r.s2 >> 4) & 0x0F0F0F0Fu) | ((r.s1 >> 2) & 0x30303030u);
     if constexpr (kFive) s.qh = r.qh;
   }
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &s) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &s) {
     const uint32_t scw = G < 2 ? s.sc03 : s.sc47, mw = G < 2 ? s.m03 : s.m47;
     constexpr bool hi = S >= 2;
     constexpr int e = (2 * G + (hi ? 1 : 0)) & 3;
@@ -154,7 +163,7 @@ struct TK45 {
       a = ((hi ? a >> 4 : a) & 0x0F0F0F0Fu) | (((ha >> bit) & 0x01010101u) << 4);
       b = ((hi ? b >> 4 : b) & 0x0F0F0F0Fu) | (((hb >> bit) & 0x01010101u) << 4);
     }
-    return fma8(a, b, dl, -ml);
+    return fma8<O>(a, b, dl, -ml);
   }
 };
 template <>
@@ -205,15 +214,15 @@ struct T<Q6_K> {
         s.ds[4 * H + p] = d * (float)v;
       }
   }
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &s) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &s) {
     constexpr int H = G >> 1, p = 2 * (G & 1) + (S >> 1), sh = 4 * (G & 1);
     const uint4 &ql = (S >> 1) ? r.qlb[H] : r.qla[H];
     const uint32_t a = ((w0of<S>(ql) >> sh) & 0x0F0F0F0Fu) | (((w0of<S>(r.qh[H]) >> (2 * p)) & 0x03030303u) << 4);
     const uint32_t b = ((w1of<S>(ql) >> sh) & 0x0F0F0F0Fu) | (((w1of<S>(r.qh[H]) >> (2 * p)) & 0x03030303u) << 4);
     const float ds = s.ds[4 * H + p];
     // d*sc*(q-32) is exact in f32 (<= 24 significant bits): fma(q, ds, -32 ds)
-    return fma8(a, b, ds, -32.f * ds);
+    return fma8<O>(a, b, ds, -32.f * ds);
   }
 };
 
@@ -261,14 +270,14 @@ struct T<Q3_K> {
       }
     s.hm = r.hm;
   }
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &s) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &s) {
     constexpr int H = G >> 1, p = 2 * (G & 1) + (S >> 1), hb = 4 * H + p;
     // 3-bit value v = q2 + 4*hbit; weight = dl * (v - 4), exact
     const uint32_t a = ((w0of<S>(r.qs[H]) >> (2 * p)) & 0x03030303u) | (((w0of<S>(s.hm) >> hb) & 0x01010101u) << 2);
     const uint32_t b = ((w1of<S>(r.qs[H]) >> (2 * p)) & 0x03030303u) | (((w1of<S>(s.hm) >> hb) & 0x01010101u) << 2);
     const float dl = s.dl[4 * H + p];
-    return fma8(a, b, dl, -4.f * dl);
+    return fma8<O>(a, b, dl, -4.f * dl);
   }
 };
 
@@ -307,11 +316,11 @@ struct T<Q2_K> {
         s.ml[4 * H + p] = dmin * (float)(v >> 4);
       }
   }
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &s) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &s) {
     constexpr int H = G >> 1, p = 2 * (G & 1) + (S >> 1);
     constexpr uint32_t M = 0x03030303u;
-    return fma8((w0of<S>(r.qs[H]) >> (2 * p)) & M, (w1of<S>(r.qs[H]) >> (2 * p)) & M, s.dl[4 * H + p],
+    return fma8<O>((w0of<S>(r.qs[H]) >> (2 * p)) & M, (w1of<S>(r.qs[H]) >> (2 * p)) & M, s.dl[4 * H + p],
                 -s.ml[4 * H + p]);
   }
 };
@@ -349,8 +358,8 @@ struct T32 {
   __device__ static uint32_t spread(uint32_t qh, int sh) {
     return ((((qh >> sh) & 15u) * 0x00204081u) & 0x01010101u) << 4;
   }
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &) {
     const float d = h2f((uint16_t)(r.d[G] & 0xFFFF));
     constexpr bool hi = S >= 2;
     uint32_t a = w0of<S>(r.q[G]), b = w1of<S>(r.q[G]);
@@ -358,13 +367,13 @@ struct T32 {
       const float add = kMin ? h2f((uint16_t)(r.d[G] >> 16)) : -8.f * d;
       const uint32_t M = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
       // high nibbles masked in place are 16*q: scale by d/16 (exact)
-      return fma8(a & M, b & M, hi ? d * 0.0625f : d, add);
+      return fma8<O>(a & M, b & M, hi ? d * 0.0625f : d, add);
     } else {
       const float add = kMin ? h2f((uint16_t)(r.d[G] >> 16)) : -16.f * d;
       constexpr int bit0 = 16 * (S >> 1) + 8 * (S & 1);
       a = ((hi ? a >> 4 : a) & 0x0F0F0F0Fu) | spread(r.qh[G], bit0);
       b = ((hi ? b >> 4 : b) & 0x0F0F0F0Fu) | spread(r.qh[G], bit0 + 4);
-      return fma8(a, b, d, add);
+      return fma8<O>(a, b, d, add);
     }
   }
 };
@@ -397,12 +406,12 @@ struct T<Q8_0> {
     r.d[G] = ld2(rec_at(w, 0, 2, t, b, row));
   }
   __device__ static void prep(const Raw &, Sc &, int) {}
-  template <int G, int S>
-  __device__ static bf16x8 frag(const Raw &r, const Sc &) {
+  template <int G, int S, typename O = bf16x8>
+  __device__ static O frag(const Raw &r, const Sc &) {
     const float d = h2f((uint16_t)r.d[G]);
     constexpr uint32_t X = 0x80808080u;
     const uint4 &q = r.q[G][S >> 1];
-    return fma8(w0of<S>(q) ^ X, w1of<S>(q) ^ X, d, -128.f * d);
+    return fma8<O>(w0of<S>(q) ^ X, w1of<S>(q) ^ X, d, -128.f * d);
   }
 };
 

@@ -376,6 +376,171 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Streaming GEMV for the other types (f32 x, exact f32 weights): the same work
+// layout as the Q4_K kernel (one 512-thread workgroup per CU over `rows`
+// consecutive output rows and all of K, thread t taking the (row, unit) pairs
+// t, t + 512, ... with the row fastest so a wave's 16-byte loads of one chunk
+// plane read consecutive rows), with the weights decoded by the GEMM's
+// per-type B-fragment decoders (mq_bfrag.h) in their f32 form: each is the
+// exact value ggml's dequantize_row_* gives, and x . w accumulates in f32.  A
+// unit is 256 weights (128 for Q8_0), split in the decoders' two halves; a
+// thread's (row, unit, half) bytes are loaded into registers as whole 16-byte
+// chunks and the next item's loads are issued before the current item is
+// computed.  x is staged to LDS by direct loads (in the shadow of the first
+// item's weight loads); the items' partials go to LDS and thread (row, m)
+// adds them in (unit, half) order (deterministic).
+constexpr int kFragThreads = 512;
+constexpr size_t kFragMaxLds = 96 * 1024;
+constexpr int kFragMaxM = 4;  // larger m takes gemv_kernel
+
+__host__ __device__ inline size_t frag_lds_bytes(int64_t k, int m, int64_t rows, int64_t units) {
+  return (size_t)m * k * 4 + ((size_t)rows * units * 2 + 1) * m * 4;
+}
+
+template <int TYPE, int M, typename OUT>
+__global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_t n, int64_t nrows_mem, int units,
+                                                                 int rows, const float *__restrict__ x, int64_t ldx,
+                                                                 OUT *__restrict__ y, int64_t ldy,
+                                                                 const float *__restrict__ bias, int act) {
+  using TT = bfrag::T<TYPE>;
+  constexpr int kU = TT::kUnitK, kP = kU / 64;
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int64_t k = (int64_t)units * kU;
+  float *xs = reinterpret_cast<float *>(smem);            // [M][k]
+  float *red = xs + (size_t)M * k;                        // [units * 2 * rows + 1][M]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int64_t r0 = (int64_t)blockIdx.x * rows;
+  // a work item is (row, unit, half h): the decoders' lane-half split, so a
+  // thread holds one half unit's bytes (item p = (2 u + h) * rows + row)
+  const int nitems = rows * units * 2;
+
+  auto load_item = [&](int p, typename TT::Raw &d) {
+    p = p < nitems ? p : nitems - 1;  // clamped: every load unconditional, in bounds
+    const int uh = p / rows;
+    int64_t row = r0 + (p - uh * rows);
+    row = row < nrows_mem ? row : nrows_mem - 1;
+    const int64_t t = row >> 6;
+    const int r = (int)(row & 63), u = uh >> 1, h = uh & 1;
+    TT::load_prep(d, w, t, r, u, h);
+    static_for<kP>([&]<int G>() { TT::template reload<G>(d, w, t, r, u, h); });
+  };
+  auto dot_item = [&](int p, const typename TT::Raw &d) {
+    const bool valid = p < nitems;
+    p = valid ? p : nitems - 1;
+    const int uh = p / rows, u = uh >> 1, h = uh & 1;
+    typename TT::Sc sc;
+    TT::prep(d, sc, h);
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.f;
+    static_for<kP>([&]<int G>() {
+      // keeps the x reads of one step together with their use
+      asm volatile("" ::: "memory");
+      static_for<4>([&]<int S>() {
+        const bfrag::f32x8 v = TT::template frag<G, S, bfrag::f32x8>(d, sc);
+        const int64_t e = (int64_t)u * kU + 64 * G + 8 * (h ? TT::chunk(S, 1) : TT::chunk(S, 0));
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const float4 xa = *reinterpret_cast<const float4 *>(xs + m * k + e);
+          const float4 xb = *reinterpret_cast<const float4 *>(xs + m * k + e + 4);
+          float a = acc[m];
+          a = __builtin_fmaf(v[0], xa.x, a);
+          a = __builtin_fmaf(v[1], xa.y, a);
+          a = __builtin_fmaf(v[2], xa.z, a);
+          a = __builtin_fmaf(v[3], xa.w, a);
+          a = __builtin_fmaf(v[4], xb.x, a);
+          a = __builtin_fmaf(v[5], xb.y, a);
+          a = __builtin_fmaf(v[6], xb.z, a);
+          a = __builtin_fmaf(v[7], xb.w, a);
+          acc[m] = a;
+        }
+      });
+    });
+    // unconditional store (a clamped item writes the spare slot): a
+    // conditional one lets the compiler sink the whole decode into the branch
+    const int slot = valid ? p : nitems;
+#pragma unroll
+    for (int m = 0; m < M; ++m) red[slot * M + m] = acc[m];
+  };
+
+  // 1. the first item's weights, then x into LDS by direct loads (item j =
+  //    row m's elements 256 c .. +255: one 1 KiB wave load), one wait for both
+  typename TT::Raw a, b;
+  load_item(tid, a);
+  {
+    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t *)smem;
+    const int items = (int)(M * (k >> 8));
+    const int64_t per_row = k >> 8;
+    for (int j = wave; j < items; j += kFragThreads / 64) {
+      const int m = (int)(j / per_row);
+      const int64_t c = j - (int64_t)m * per_row;
+      dma16(x + m * ldx + c * 256 + 4 * lane, lbase + (uint32_t)j * 1024);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  // 2. items, the next one's loads in flight while the current one computes
+  for (int p = tid;; p += 2 * kFragThreads) {
+    load_item(p + kFragThreads, b);
+    dot_item(p, a);
+    if (p + kFragThreads >= nitems) break;
+    load_item(p + 2 * kFragThreads, a);
+    dot_item(p + kFragThreads, b);
+    if (p + 2 * kFragThreads >= nitems) break;
+  }
+  __syncthreads();
+
+  // 3. thread (row, m) adds its row's partials in (unit, half) order
+  for (int t = tid; t < rows * M; t += kFragThreads) {
+    const int m = t / rows, rl = t - m * rows;
+    const int64_t row = r0 + rl;
+    if (row >= n) continue;
+    float acc = 0.f;
+    for (int uh = 0; uh < 2 * units; ++uh) acc += red[(uh * rows + rl) * M + m];
+    if (bias) acc += bias[row];
+    store1<OUT>(y + m * ldy + row, apply_act(acc, act));
+  }
+}
+
+// Rows per workgroup of the streaming kernel (0: use gemv_kernel): one
+// workgroup per CU; x and the partials must fit the LDS.
+static int frag_rows(int type, int64_t n, int64_t k, int64_t m, int cus) {
+  const int64_t unit = type == Q8_0 ? 128 : 256;
+  if (type == Q4_K || k % 256 != 0 || m > kFragMaxM) return 0;
+  if ((type == Q5_K || type == Q6_K) && m > 3) return 0;  // their m = 4 instances spill
+  int64_t rows = (n + cus - 1) / cus;
+  if (rows < 1) rows = 1;
+  while (rows > 8 && frag_lds_bytes(k, (int)m, rows, k / unit) > kFragMaxLds) rows = (rows + 1) / 2;
+  if (frag_lds_bytes(k, (int)m, rows, k / unit) > kFragMaxLds) return 0;
+  return (int)rows;
+}
+
+template <int TYPE, int M, typename OUT>
+static void launch_gemv_frag(const WView &w, int64_t n, int64_t k, const float *x, int64_t ldx, OUT *y, int64_t ldy,
+                             const float *bias, int act, int rows, hipStream_t stream) {
+  constexpr int64_t unit = bfrag::T<TYPE>::kUnitK;
+  const int units = (int)(k / unit);
+  const int64_t wgs = (n + rows - 1) / rows;
+  const int64_t nrows_mem = ((n + kRowTile - 1) / kRowTile) * kRowTile;
+  hipLaunchKernelGGL((gemv_frag_kernel<TYPE, M, OUT>), dim3((unsigned)wgs), dim3(kFragThreads),
+                     frag_lds_bytes(k, M, rows, units), stream, w, n, nrows_mem, units, rows, x, ldx, y, ldy, bias,
+                     act);
+}
+
+template <int TYPE, typename OUT>
+static void launch_gemv_frag_m(const WView &w, int64_t n, int64_t k, const float *x, int64_t m, int64_t ldx, OUT *y,
+                               int64_t ldy, const float *bias, int act, int rows, hipStream_t stream) {
+  switch (m) {
+    case 1: launch_gemv_frag<TYPE, 1, OUT>(w, n, k, x, ldx, y, ldy, bias, act, rows, stream); break;
+    case 2: launch_gemv_frag<TYPE, 2, OUT>(w, n, k, x, ldx, y, ldy, bias, act, rows, stream); break;
+    case 3: launch_gemv_frag<TYPE, 3, OUT>(w, n, k, x, ldx, y, ldy, bias, act, rows, stream); break;
+    default: launch_gemv_frag<TYPE, 4, OUT>(w, n, k, x, ldx, y, ldy, bias, act, rows, stream); break;
+  }
+}
+
 // Rows per workgroup of the Q4_K path (0: use the generic kernel): one
 // workgroup per CU, fewer rows when the LDS would not hold them.
 static int q4k_rows(int64_t n, int64_t nb, int64_t m, int cus) {
@@ -408,6 +573,7 @@ static int pick_ksplit(int64_t ntiles, int64_t k) {
 
 size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k, int cus) {
   if (type == Q4_K && q4k_rows(n, k / 256, m, cus)) return 0;
+  if (frag_rows(type, n, k, m, cus)) return 0;
   const int64_t ntiles = (n + kRowTile - 1) / kRowTile;
   const int ks = pick_ksplit(ntiles, k);
   if (ks == 1) return 0;
@@ -418,7 +584,7 @@ template <int TYPE, int M, typename OUT>
 static void launch_gemv_t(const WView &w, int64_t n, int64_t k, const float *x, int64_t ldx, OUT *y,
                           int64_t ldy, const float *bias, int act, float *partial, hipStream_t stream) {
   const int64_t ntiles = (n + kRowTile - 1) / kRowTile;
-  const int ks = pick_ksplit(ntiles, k);
+  const int ks = partial ? pick_ksplit(ntiles, k) : 1;  // no partials buffer: whole K per workgroup
   const int64_t npad = ntiles * kRowTile;
   hipLaunchKernelGGL((gemv_kernel<TYPE, M, OUT>), dim3((unsigned)ntiles, ks), dim3(kGemvWaves * 64), 0,
                      stream, w, n, k, x, ldx, y, ldy, bias, act, partial, ks, npad);
@@ -493,8 +659,22 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const voi
     }
     return hipGetLastError();
   }
-  if (x_type != F32) return hipErrorInvalidValue;  // the generic kernel reads f32 x
+  if (x_type != F32) return hipErrorInvalidValue;  // the other kernels read f32 x
   const float *xf = static_cast<const float *>(x);
+  const int frows = frag_rows(type, n, k, m, cus);
+  if (frows && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0) {
+    bool ok = dispatch_type(type, [&]<int T>() {
+      if constexpr (T != Q4_K) {
+        if (y_type == F32)
+          launch_gemv_frag_m<T, float>(w, n, k, xf, m, ldx, static_cast<float *>(y), ldy, bias, act, frows, stream);
+        else
+          launch_gemv_frag_m<T, __bf16>(w, n, k, xf, m, ldx, static_cast<__bf16 *>(y), ldy, bias, act, frows,
+                                        stream);
+      }
+    });
+    if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   bool ok = dispatch_type(type, [&]<int T>() {
     if (y_type == F32)
       launch_gemv_m<T, float>(w, n, k, xf, m, ldx, static_cast<float *>(y), ldy, bias, act, partial, stream);
