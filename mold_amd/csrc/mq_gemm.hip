@@ -13,11 +13,11 @@
 //     the MFMA B operand (per-type decoders, mq_bfrag.h), so every weight is
 //     decoded once per block tile and B never touches LDS;
 //   * v_mfma_f32_32x32x16_bf16, 8 accumulator tiles (128 f32) per lane;
-//   * the bf16 activation tile (256 x 64 per K step) goes global -> VGPR ->
-//     LDS one step ahead through a 2-slot ring (2 x 32 KiB per workgroup),
-//     with buffer loads whose range check turns rows past m into zeros;
-//     every memory operation is visible to the compiler, so its waits are
-//     exact and loads stay in flight across the step barrier;
+//   * the bf16 activation tile (256 x 64 per K step) goes global -> LDS one
+//     step ahead by LDS DMA (global_load_lds_dwordx4: no VGPRs, no LDS
+//     write instructions) through a 2-slot ring (2 x 32 KiB per workgroup);
+//     the step's weight loads are issued with it at the step's start and
+//     both are awaited once, at the step barrier;
 //   * rows are 128 B, chunk c of row r in slot c ^ ((r >> 1) & 7), so the
 //     16 lanes of a ds_read_b128 / ds_write_b128 quarter hit distinct banks;
 //   * XCD-aware tile order: workgroup i runs on XCD i % 8; each XCD gets a
@@ -210,17 +210,24 @@ constexpr int kFM = kGemmTileM, kFN = kGemmTileN, kFK = 64;
 constexpr int kFastThreads = 256;
 constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
 
-// Raw buffer resource over `bytes` bytes at p (gfx9 untyped buffer: loads
-// past `bytes` return 0 and stores past it are dropped).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+// 16 bytes per lane from sbase + voff straight into LDS: lane i of the wave
+// writes LDS bytes lds + 16 i .. + 15 (global_load_lds_dwordx4, saddr form).
+// sbase and lds must be wave-uniform.  The compiler does not track this load:
+// its data may be read only after step_barrier.
+__device__ __forceinline__ void dma16(const char *sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
 }
 
-// Barrier between K steps: this wave's LDS writes and reads are complete,
-// every wave has arrived; global loads stay in flight (__syncthreads would
-// wait for them).  The memory clobber keeps the compiler from moving LDS
-// accesses across it.
-__device__ __forceinline__ void step_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Barrier between K steps: every load of this wave (weights and the LDS DMA
+// of the next A tile) has landed and its LDS reads are complete, then every
+// wave arrives.  The wait is the s_waitcnt builtin, so the compiler knows the
+// weight loads are complete and adds no waits of its own before their use;
+// the memory clobber keeps LDS accesses from moving across the barrier.
+__device__ __forceinline__ void step_barrier() {
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) expcnt(7) lgkmcnt(0)
+  asm volatile("s_barrier" ::: "memory");
+}
 
 template <int TYPE, typename OUT, bool GATED>
 __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
@@ -267,29 +274,30 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
 
-  // A staging: thread -> 16-byte chunk ac of rows ar + 32 i (i = 0..7) of the
-  // 256 x 64 step tile, moved in two halves (i < 4, i >= 4) of four loads so
-  // that only 16 VGPRs hold A in flight.  The row's byte offset is the buffer
-  // load's voffset (range-checked: rows >= m read 0); the K offset is uniform
-  // (soffset).
+  // A staging by LDS DMA: load i (0..7) of wave `wave` fills LDS rows
+  // 32 i + 8 wave .. +7 of a slot (1 KiB), lane -> row ar = tid / 8, LDS
+  // chunk slot ac = tid % 8, so the lane fetches global chunk
+  // ac ^ ((ar >> 1) & 7) ((ar + 32 i) >> 1 & 7 == ar >> 1 & 7).  Rows past m
+  // re-read row m - 1: their products land only in accumulator rows that are
+  // never stored.  Row offsets are per lane (voff), the K offset is in the
+  // uniform base address.
   const int ac = tid & 7, ar = tid >> 3;
-  const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(a, (uint32_t)(m * lda * 2));
-  const uint32_t avoff = (uint32_t)(((m0 + ar) * lda + ac * 8) * 2);
-  const uint32_t arow = (uint32_t)(32 * lda * 2);
+  const int gch = ac ^ ((ar >> 1) & 7);
+  uint32_t voff[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t r = m0 + ar + 32 * i < m ? m0 + ar + 32 * i : m - 1;
+    voff[i] = (uint32_t)((r * lda + gch * 8) * 2);
+  }
   const uint32_t akb = (uint32_t)(ub * TT::kUnitK * 2);
-  uint4 ast[4];
-  auto load_a = [&](int64_t ks, int half) {
-    const uint32_t kb = akb + (uint32_t)ks * (kFK * 2);
+  const uint32_t lds_wave = (uint32_t)(uintptr_t)(&lds_a[0][0]) + (uint32_t)(8 * 128 * wave);
+  auto dma_a = [&](int64_t ks, int slot) {
+    const uint64_t g = reinterpret_cast<uint64_t>(a) + akb + (uint64_t)ks * (kFK * 2);
+    const char *sb = reinterpret_cast<const char *>(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32)) << 32) |
+                                                    (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      auto t = __builtin_amdgcn_raw_buffer_load_b128(arsrc, avoff + (4 * half + i) * arow, kb, 0);
-      __builtin_memcpy(&ast[i], &t, 16);
-    }
-  };
-  const int sw_st = ac ^ ((ar >> 1) & 7);  // (ar + 32 i) >> 1 & 7 == ar >> 1 & 7
-  auto store_a = [&](int slot, int half) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lds_a[slot][(ar + 32 * (4 * half + i)) * 8 + sw_st] = ast[i];
+    for (int i = 0; i < 8; ++i)
+      dma16(sb, voff[i], __builtin_amdgcn_readfirstlane(lds_wave + (uint32_t)(slot * (kFM * kFK * 2) + 32 * 128 * i)));
   };
   const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
   auto read_a = [&](int slot, int mb, int S) -> bf16x8 {
@@ -303,23 +311,29 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   // prologue: unit 0's weight bytes and scales, A(0) into slot 0
   TT::load_prep(raw, w, wt, wrow, ub, h);
   static_for<kP>([&]<int G>() { TT::template reload<G>(raw, w, wt, wrow, ub, h); });
-  load_a(0, 0);
-  store_a(0, 0);
-  load_a(0, 1);
-  store_a(0, 1);
+  dma_a(0, 0);
   TT::prep(raw, sc, h);
   step_barrier();
 
+  // Every load a step issues (A(ks+1) into the other slot, the weight piece
+  // decoded in the previous step and, at a unit's first step, the next unit's
+  // scale bytes) is issued at the step's start and awaited at its end, so each
+  // has a whole step of MFMAs to land.  Piece G is last used in step G (kP >= 2
+  // for every type), so at step G piece G-1 is free to take the next unit's
+  // bytes, and at step 0 piece kP-1 takes this unit's.
   for (int64_t u = 0; u < units; ++u) {
     const int64_t un = u + 1 < units ? u + 1 : u;  // the last unit re-reads itself
     static_for<kP>([&]<int G>() {
       const int64_t ks = u * kP + G;
       const int64_t kn = ks + 1 < ksteps ? ks + 1 : ks;  // the last step re-reads itself
       const int slot = (int)(ks & 1);
-      // A(ks+1) goes into the other slot (read last in step ks-1), in two
-      // halves: the first half's loads are in flight during slices 0-1, the
-      // second's during slices 2-3
-      load_a(kn, 0);
+      if constexpr (G == 0) {
+        TT::template reload<kP - 1>(raw, w, wt, wrow, ub + u, h);
+        TT::load_prep(raw, w, wt, wrow, ub + un, h);  // unpacked by prep after step kP-1
+      } else {
+        TT::template reload<G - 1>(raw, w, wt, wrow, ub + un, h);
+      }
+      dma_a(kn, slot ^ 1);  // the other slot was last read in step ks-1
       bf16x8 bf[2];
       bf[0] = TT::template frag<G, 0>(raw, sc);
       static_for<4>([&]<int S>() {
@@ -327,17 +341,8 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
 #pragma unroll
         for (int mb = 0; mb < 8; ++mb)
           acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_a(slot, mb, S), bf[S & 1], acc[mb], 0, 0, 0);
-        if constexpr (S == 1) {
-          store_a(slot ^ 1, 0);
-          load_a(kn, 1);
-        }
       });
-      // piece G of unit u is fully decoded: fetch it for unit u+1 (and, after
-      // step 0, unit u+1's scale bytes, unpacked after its last step)
-      TT::template reload<G>(raw, w, wt, wrow, ub + un, h);
-      if constexpr (G == 0) TT::load_prep(raw, w, wt, wrow, ub + un, h);
       if constexpr (G == kP - 1) TT::prep(raw, sc, h);
-      store_a(slot ^ 1, 1);
       step_barrier();
     });
   }
