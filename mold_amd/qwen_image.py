@@ -51,6 +51,7 @@ not a multiple of 256) a dense bf16 weight.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
@@ -438,18 +439,38 @@ class QwenImageStep:
         L, lt = img.shape[0] // B, txt.shape[0] // B
         H = cfg.num_attention_heads
         im = [r.chunk(6, dim=-1) for r in P.lin[p + "img_mod.1"].forward(ts)]      # M = B GEMV
-        tm = [r.chunk(6, dim=-1) for r in P.lin[p + "txt_mod.1"].forward(ts)]
-        y = P.lin[p + "attn.to_qkv"].forward(self._mod_rows(img, im, 0, 1, B), out_dtype=torch.bfloat16)
-        ty = P.lin[p + "attn.add_qkv_proj"].forward(self._mod_rows(txt, tm, 0, 1, B), out_dtype=torch.bfloat16)
+        t_mod_all = P.lin[p + "txt_mod.1"].forward(ts)
+        tm = [r.chunk(6, dim=-1) for r in t_mod_all]
         total = lt + L
+        heads_b = [new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total)
+                   for _ in range(B)]
         i_att = torch.empty((B * L, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
         t_att = torch.empty((B * lt, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
+        # text stream on `aux` as in block(): its modulate, qkv projection and
+        # q/k norm overlap the image qkv projection, its tail overlaps the image
+        # out-projection and MLP; tensors shared across the streams are recorded
+        # on the reader
+        aux = self._aux(img)
+        main = torch.cuda.current_stream(img.device) if aux is not None else None
+        on_aux = (lambda: torch.cuda.stream(aux)) if aux is not None else contextlib.nullcontext
+        if aux is not None:
+            aux.wait_stream(main)
+        with on_aux():
+            ty = P.lin[p + "attn.add_qkv_proj"].forward(self._mod_rows(txt, tm, 0, 1, B), out_dtype=torch.bfloat16)
+            for b in range(B):
+                qk_norm_rope(ty[b * lt:(b + 1) * lt], H, P.dense[p + "attn.norm_added_q.weight"],
+                             P.dense[p + "attn.norm_added_k.weight"], txt_cos, txt_sin, *heads_b[b], 0, cfg.norm_eps)
+        if aux is not None:
+            for t in (txt, t_mod_all) + tuple(t for hb in heads_b for t in hb):
+                t.record_stream(aux)
+        y = P.lin[p + "attn.to_qkv"].forward(self._mod_rows(img, im, 0, 1, B), out_dtype=torch.bfloat16)
         for b in range(B):
-            heads = new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total)
-            qk_norm_rope(ty[b * lt:(b + 1) * lt], H, P.dense[p + "attn.norm_added_q.weight"],
-                         P.dense[p + "attn.norm_added_k.weight"], txt_cos, txt_sin, *heads, 0, cfg.norm_eps)
             qk_norm_rope(y[b * L:(b + 1) * L], H, P.dense[p + "attn.norm_q.weight"], P.dense[p + "attn.norm_k.weight"],
-                         img_cos, img_sin, *heads, lt, cfg.norm_eps)
+                         img_cos, img_sin, *heads_b[b], lt, cfg.norm_eps)
+        if aux is not None:
+            main.wait_stream(aux)
+        for b in range(B):
+            heads = heads_b[b]
             drop = None
             if valid[b] < lt:
                 drop = (valid[b], lt)
@@ -462,14 +483,21 @@ class QwenImageStep:
                 a = _attention_chunked(*(t[:, :total] for t in heads), drop)
             t_att[b * lt:(b + 1) * lt] = a[:lt]
             i_att[b * L:(b + 1) * L] = a[lt:]
-        txt = self._gated_rows(p + "attn.to_add_out", t_att, tm, 2, txt, B)
-        h = P.lin[p + "txt_mlp.net.0.proj"].forward(self._mod_rows(txt, tm, 3, 4, B), act=ACT_GELU_TANH,
-                                                    out_dtype=torch.bfloat16)
-        txt = self._gated_rows(p + "txt_mlp.net.2", h, tm, 5, txt, B)
+        if aux is not None:
+            aux.wait_stream(main)
+        with on_aux():
+            txt = self._gated_rows(p + "attn.to_add_out", t_att, tm, 2, txt, B)
+            ht = P.lin[p + "txt_mlp.net.0.proj"].forward(self._mod_rows(txt, tm, 3, 4, B), act=ACT_GELU_TANH,
+                                                         out_dtype=torch.bfloat16)
+            txt = self._gated_rows(p + "txt_mlp.net.2", ht, tm, 5, txt, B)
+        if aux is not None:
+            t_att.record_stream(aux)
         img = self._gated_rows(p + "attn.to_out.0", i_att, im, 2, img, B)
         h = P.lin[p + "img_mlp.net.0.proj"].forward(self._mod_rows(img, im, 3, 4, B), act=ACT_GELU_TANH,
                                                     out_dtype=torch.bfloat16)
         img = self._gated_rows(p + "img_mlp.net.2", h, im, 5, img, B)
+        if aux is not None:
+            main.wait_stream(aux)
         return img, txt
 
     def _forward_batched(self, img, txt, t, grid, valid, blocks):
