@@ -128,8 +128,9 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 // (row, super-block) pairs p = t, t + 512, ... (row fastest, so a wave's
 // 16-byte loads of one chunk plane read consecutive rows of the tiled
 // layout), and issues the loads of its first pair before anything else:
-// the weight stream starts at once and the Q8_K staging of x (wave j
-// quantizes super-blocks j, j+8, ... into LDS) runs while it is in flight.
+// the weight stream starts at once and the Q8_K staging of x runs while it is
+// in flight: 16-lane group g (of 32) quantizes items g, g + 32, ... (item =
+// one row of x over one super-block) into LDS, 16 elements per lane.
 // Each pair's integer dot reads its 32 Q8_K bytes per 16-byte weight chunk
 // from LDS: 3 + 2M VALU ops per 8 weights.  The pairs' f32 partials go to
 // LDS and thread (row, m) adds them in super-block order (deterministic).
@@ -142,24 +143,20 @@ template <int CTRL, int ROW_MASK>
 __device__ __forceinline__ int dpp(int v) {
   return __builtin_amdgcn_update_dpp(v, v, CTRL, ROW_MASK, 0xF, false);
 }
-// Max over the wave, uniform: quad xor 1, quad xor 2, half-row mirror, row
-// mirror give every lane its 16-lane row's max; row_bcast:15 (rows 1, 3) and
-// row_bcast:31 (rows 2, 3) carry rows 0-2 into row 3; lane 63 holds the max.
-__device__ __forceinline__ float wave_max(float v) {
+// Max / min over each aligned group of 16 lanes (a DPP row), in every lane of
+// it: quad xor 1, quad xor 2, half-row mirror (quads 0 <-> 1), row mirror
+// (half rows 0 <-> 1).
+__device__ __forceinline__ float row16_max(float v) {
   v = __builtin_fmaxf(v, __int_as_float(dpp<0xB1, 0xF>(__float_as_int(v))));
   v = __builtin_fmaxf(v, __int_as_float(dpp<0x4E, 0xF>(__float_as_int(v))));
   v = __builtin_fmaxf(v, __int_as_float(dpp<0x141, 0xF>(__float_as_int(v))));
-  v = __builtin_fmaxf(v, __int_as_float(dpp<0x140, 0xF>(__float_as_int(v))));
-  v = __builtin_fmaxf(v, __int_as_float(dpp<0x142, 0xA>(__float_as_int(v))));
-  v = __builtin_fmaxf(v, __int_as_float(dpp<0x143, 0xC>(__float_as_int(v))));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  return __builtin_fmaxf(v, __int_as_float(dpp<0x140, 0xF>(__float_as_int(v))));
 }
-// Sum over each aligned group of 8 lanes (a half row), in every lane of it.
-__device__ __forceinline__ int sum8(int v) {
-  v += dpp<0xB1, 0xF>(v);
-  v += dpp<0x4E, 0xF>(v);
-  v += dpp<0x141, 0xF>(v);
-  return v;
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp<0xB1, 0xF>(v));
+  v = min(v, dpp<0x4E, 0xF>(v));
+  v = min(v, dpp<0x141, 0xF>(v));
+  return min(v, dpp<0x140, 0xF>(v));
 }
 
 // LDS of the Q4_K GEMV: x as given (f32 or bf16, 256 elements per
@@ -254,39 +251,71 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
   __syncthreads();
 
-  // 2. Q8_K staging: lane L holds elements 4L..4L+3 (sub-block L / 8)
+  // 2. Q8_K staging: one item per 16-lane group (32 groups, every one at
+  //    once); lane L of a group holds elements 16L..16L+15, half of sub-block
+  //    L / 2.
+  const int g16 = tid >> 4, l16 = tid & 15;
   auto stage = [&](int j) {
-    float v[4];
+    float v[16];
+    if constexpr (kXs == 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (float)xl[j * 256 + 4 * lane + i];
-    // largest magnitude over the wave, then the value of its first
-    // occurrence in element order (lowest lane, lowest slot in the lane)
-    const float a0 = __builtin_fabsf(v[0]), a1 = __builtin_fabsf(v[1]);
-    const float a2 = __builtin_fabsf(v[2]), a3 = __builtin_fabsf(v[3]);
-    const float amax = wave_max(__builtin_fmaxf(__builtin_fmaxf(a0, a1), __builtin_fmaxf(a2, a3)));
-    const float cand = a0 == amax ? v[0] : a1 == amax ? v[1] : a2 == amax ? v[2] : v[3];
-    const uint64_t hit = __ballot(a0 == amax || a1 == amax || a2 == amax || a3 == amax);
-    const int first = hit ? __builtin_ctzll(hit) : 0;
-    const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(cand), first));
-    uint32_t packed = 0;
+      for (int c = 0; c < 4; ++c) {
+        const float4 t = *reinterpret_cast<const float4 *>(xl + j * 256 + 16 * l16 + 4 * c);
+        v[4 * c] = t.x;
+        v[4 * c + 1] = t.y;
+        v[4 * c + 2] = t.z;
+        v[4 * c + 3] = t.w;
+      }
+    } else {
+      // bf16 -> f32 is exact: the 16 bits become the high half
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint4 t = *reinterpret_cast<const uint4 *>(xl + j * 256 + 16 * l16 + 8 * c);
+        const uint32_t wd[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[8 * c + 2 * i] = __uint_as_float(wd[i] << 16);
+          v[8 * c + 2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+        }
+      }
+    }
+    // largest magnitude over the item, then the value of its first occurrence
+    // in element order: the lowest element index holding it, taken from the
+    // lane that owns that index (with no hit, as for an all-NaN item, element 3)
+    float lmax = __builtin_fabsf(v[0]);
+#pragma unroll
+    for (int i = 1; i < 16; ++i) lmax = __builtin_fmaxf(lmax, __builtin_fabsf(v[i]));
+    const float amax = row16_max(lmax);
+    int first = 16;
+    float cand = v[3];
+#pragma unroll
+    for (int i = 15; i >= 0; --i) {
+      const bool hit = __builtin_fabsf(v[i]) == amax;
+      first = hit ? i : first;
+      cand = hit ? v[i] : cand;
+    }
+    const int gfirst = row16_min(first < 16 ? 16 * l16 + first : 256);
+    const int src = (tid & 63 & ~15) + (gfirst < 256 ? gfirst >> 4 : 0);
+    const float vmax = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(cand)));
+    uint32_t packed[4] = {0u, 0u, 0u, 0u};
     int qsum = 0;
     float dx = 0.f;
     if (amax != 0.f) {
       const float iscale = -128.f / vmax;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 16; ++i) {
         const int q = (int)__builtin_fminf(__builtin_roundf(iscale * v[i]), 127.f);
         qsum += q;
-        packed |= (uint32_t)(q & 0xFF) << (8 * i);
+        packed[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
       }
       dx = 1.f / iscale;
     }
-    xq[j * 64 + lane] = packed;
-    qsum = sum8(qsum);
-    if ((lane & 7) == 0) xs[j * 8 + (lane >> 3)] = qsum;
-    if (lane == 0) xd[j] = dx;
+    *reinterpret_cast<uint4 *>(xq + j * 64 + 4 * l16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    qsum += dpp<0xB1, 0xF>(qsum);  // the sub-block's other half (lane L ^ 1)
+    if ((l16 & 1) == 0) xs[j * 8 + (l16 >> 1)] = qsum;
+    if (l16 == 0) xd[j] = dx;
   };
-  for (int j = wave; j < nitems; j += kWaves) stage(j);
+  for (int j = g16; j < nitems; j += kQ4kThreads / 16) stage(j);
   __syncthreads();
 
   // 3. per pair: integer dot against Q8_K x, one f32 partial per m
