@@ -223,10 +223,10 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
 
   // 1. x into LDS by direct loads (item j = sb * M + m is row m's elements
   //    sb*256 .. +255: one 1 KiB load for f32, half a wave's for bf16), then
-  //    the first two pairs' weights (indices clamped, so every load is
-  //    unconditional).  The explicit wait below leaves the 20 loads issued
-  //    after x's in flight (two pairs: 8 chunk loads, d/dmin and the scale
-  //    record each, none of which can merge), so only x has landed.
+  //    the first pair's weights (index clamped, so every load is
+  //    unconditional).  The explicit wait below leaves the 10 loads issued
+  //    after x's in flight (8 chunk loads, d/dmin and the scale record, none
+  //    of which can merge), so only x has landed.
   const int nitems = nb * M;
   constexpr int kWaves = kQ4kThreads / 64;
   {
@@ -247,8 +247,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   }
   Q4kPair slot[2];
   load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
-  load_pair(tid + kQ4kThreads < npairs ? tid + kQ4kThreads : npairs - 1, slot[1]);
-  asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
   __syncthreads();
 
   // 2. Q8_K staging: one item per 16-lane group (32 groups, every one at
@@ -337,28 +336,36 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     int S[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) S[m] = 0;
+    if constexpr (M <= 2) {
+      // steps s = (g, m) in order g-major: chunks 2g and 2g+1 (32 bytes) hold
+      // elements 64g + 0..31 in their low nibbles (sub-block 2g) and 64g +
+      // 32..63 in their high nibbles (sub-block 2g+1), each in byte order; one
+      // sdot4 chain of 8 per sub-block and row m of x.  The 64 Q8_K bytes of
+      // step s + 1 are read from LDS while step s computes (two register slots).
+      auto xload = [&](int g, int m, uint4 *dst) {
+        const uint4 *xb = reinterpret_cast<const uint4 *>(xq + (sb * M + m) * 64 + 16 * g);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      // chunks 2g and 2g+1 (32 bytes): low nibbles are elements 64g + 0..31
-      // (sub-block 2g), high nibbles elements 64g + 32..63 (sub-block 2g+1),
-      // each in byte order; one sdot4 chain of 8 per sub-block
-      const uint32_t wd[8] = {cur.q[2 * g].x,     cur.q[2 * g].y,     cur.q[2 * g].z,     cur.q[2 * g].w,
-                              cur.q[2 * g + 1].x, cur.q[2 * g + 1].y, cur.q[2 * g + 1].z, cur.q[2 * g + 1].w};
+        for (int i = 0; i < 4; ++i) dst[i] = xb[i];
+      };
+      uint4 xbuf[2][4];
+      xload(0, 0, xbuf[0]);
       uint32_t lo[8], hi[8];
+      static_for<4 * M>([&]<int ST>() {
+        constexpr int g = ST / M, m = ST % M;
+        if constexpr (ST + 1 < 4 * M) xload((ST + 1) / M, (ST + 1) % M, xbuf[(ST + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of this step's dots
+        if constexpr (m == 0) {
+          const uint32_t wd[8] = {cur.q[2 * g].x,     cur.q[2 * g].y,     cur.q[2 * g].z,     cur.q[2 * g].w,
+                                  cur.q[2 * g + 1].x, cur.q[2 * g + 1].y, cur.q[2 * g + 1].z, cur.q[2 * g + 1].w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        lo[i] = wd[i] & 0x0F0F0F0Fu;
-        hi[i] = (wd[i] >> 4) & 0x0F0F0F0Fu;
-      }
-#pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const uint32_t *xb = xq + (sb * M + m) * 64 + 16 * g;
-        const uint4 x0 = *reinterpret_cast<const uint4 *>(xb);
-        const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 4);
-        const uint4 x2 = *reinterpret_cast<const uint4 *>(xb + 8);
-        const uint4 x3 = *reinterpret_cast<const uint4 *>(xb + 12);
-        const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+          for (int i = 0; i < 8; ++i) {
+            lo[i] = wd[i] & 0x0F0F0F0Fu;
+            hi[i] = (wd[i] >> 4) & 0x0F0F0F0Fu;
+          }
+        }
+        const uint4 *xv = xbuf[ST & 1];
+        const uint32_t xl[8] = {xv[0].x, xv[0].y, xv[0].z, xv[0].w, xv[1].x, xv[1].y, xv[1].z, xv[1].w};
+        const uint32_t xh[8] = {xv[2].x, xv[2].y, xv[2].z, xv[2].w, xv[3].x, xv[3].y, xv[3].z, xv[3].w};
         int dl = 0, dh = 0;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -367,6 +374,41 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
         }
         // |dl|, |dh| <= 32 * 15 * 128 < 2^16: the 24-bit products are exact
         S[m] += __mul24(sc[2 * g], dl) + __mul24(sc[2 * g + 1], dh);
+      });
+    } else {
+      // (m > 2: the same steps with the Q8_K bytes read at their use; two
+      // register slots of 16 per step would spill at these m)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        // chunks 2g and 2g+1 (32 bytes): low nibbles are elements 64g + 0..31
+        // (sub-block 2g), high nibbles elements 64g + 32..63 (sub-block 2g+1),
+        // each in byte order; one sdot4 chain of 8 per sub-block
+        const uint32_t wd[8] = {cur.q[2 * g].x,     cur.q[2 * g].y,     cur.q[2 * g].z,     cur.q[2 * g].w,
+                                cur.q[2 * g + 1].x, cur.q[2 * g + 1].y, cur.q[2 * g + 1].z, cur.q[2 * g + 1].w};
+        uint32_t lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          lo[i] = wd[i] & 0x0F0F0F0Fu;
+          hi[i] = (wd[i] >> 4) & 0x0F0F0F0Fu;
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const uint32_t *xb = xq + (sb * M + m) * 64 + 16 * g;
+          const uint4 x0 = *reinterpret_cast<const uint4 *>(xb);
+          const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 4);
+          const uint4 x2 = *reinterpret_cast<const uint4 *>(xb + 8);
+          const uint4 x3 = *reinterpret_cast<const uint4 *>(xb + 12);
+          const uint32_t xl[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          const uint32_t xh[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+          int dl = 0, dh = 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            dl = __builtin_amdgcn_sdot4((int)lo[i], (int)xl[i], dl, false);
+            dh = __builtin_amdgcn_sdot4((int)hi[i], (int)xh[i], dh, false);
+          }
+          // |dl|, |dh| <= 32 * 15 * 128 < 2^16: the 24-bit products are exact
+          S[m] += __mul24(sc[2 * g], dl) + __mul24(sc[2 * g + 1], dh);
+        }
       }
     }
     const float d = h2f((uint16_t)(cur.dm & 0xFFFF)), dmin = h2f((uint16_t)(cur.dm >> 16));
@@ -383,10 +425,22 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
       if (valid) red[p * M + m] = __builtin_fmaf(d * dx, (float)S[m], -(dmin * dx) * (float)smin);
     }
   };
-  // the two preloaded pairs run straight-line (so each waits only for its
-  // own loads); pairs past them (K beyond 2 * 512 pairs) load as they go
+  // The second pairs (512 .. min(npairs, 1024) - 1, spread evenly over the
+  // waves: lanes 0 .. per-1 of each) are issued only once the first pair has
+  // landed, and the first pair's dot runs while they stream in.  All of a
+  // launch's loads issued at once finish in an arbitrary order across the
+  // chip, so each thread's pairs would land near the end of the stream and
+  // every dot would run after it; in two waves the first pairs land at about
+  // the middle and only the second pairs' dots follow the stream.  Pairs past
+  // 1024 (K beyond 2 * 512 pairs' worth) load as they go.
+  const int n2 = (npairs < 2 * kQ4kThreads ? npairs : 2 * kQ4kThreads) - kQ4kThreads;
+  const int per = n2 > 0 ? (n2 + kWaves - 1) / kWaves : 0;
+  const int p1 = kQ4kThreads + per * wave + lane;
+  const bool has1 = lane < per && p1 < npairs;
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first pair has landed
+  if (has1) load_pair(p1, slot[1]);
   dot_pair(tid, slot[0]);
-  dot_pair(tid + kQ4kThreads, slot[1]);
+  if (has1) dot_pair(p1, slot[1]);
   for (int p = tid + 2 * kQ4kThreads; p < npairs; p += kQ4kThreads) {
     load_pair(p, slot[0]);
     dot_pair(p, slot[0]);
