@@ -341,6 +341,45 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
     return _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid], drop)
 
 
+_NPAD_CACHE: dict = {}
+
+
+def attention_bf16_batch(q, k, v, valid: int, guard, drops):
+    """attention_bf16 over a batch in one fused launch: q, k, v bf16 [B, H, L, D]
+    (contiguous), rows valid .. L-1 of every element zero padding, drops[b] =
+    (lo, hi) or None the masked keys of element b (zero k and v rows).  Each
+    element's output is corrected by its own share s_b = 1 - n_b exp(-lse),
+    n_b its padded plus dropped keys, and `guard` (required here) is raised to
+    the largest 1 - s seen.  Returns [B, valid, H*D] bf16.  Without a guard, or
+    where no fused kernel serves the device, each element goes through
+    attention_bf16 (which recomputes ill-conditioned rows itself)."""
+    import torch
+    b_, h, l, d = q.shape
+    per_element = lambda: torch.stack([attention_bf16(q[b], k[b], v[b], valid=valid, guard=guard, drop=drops[b])
+                                       for b in range(b_)])
+    if guard is None or ATTENTION_BACKEND["name"] not in (None, "fused"):
+        return per_element()
+    try:
+        out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(q, k, v, None, True)[:2]
+    except RuntimeError as err:
+        if not _no_fused_kernel(err):
+            raise
+        ATTENTION_BACKEND["name"] = "chunked"
+        return per_element()
+    counts = tuple(l - valid + (0 if dr is None else max(0, dr[1] - dr[0])) for dr in drops)
+    key = (q.device, counts)
+    npad = _NPAD_CACHE.get(key)
+    if npad is None:   # one small upload per distinct padding, not per call
+        npad = torch.tensor(counts, dtype=torch.float32, device=q.device).view(b_, 1, 1)
+        _NPAD_CACHE[key] = npad
+    pad_share = npad * torch.exp(-lse[:, :, :valid])          # [B, h, valid] f32, 1 - s
+    res = torch.empty((b_, valid, h, d), dtype=torch.bfloat16, device=q.device)
+    torch.mul(out[:, :, :valid].transpose(1, 2), (1.0 / (1.0 - pad_share)).transpose(1, 2)[..., None], out=res)
+    torch.maximum(guard, pad_share.amax(), out=guard)
+    ATTENTION_BACKEND["name"] = "fused"
+    return res.reshape(b_, valid, h * d)
+
+
 def attention_f32(q, k, v):
     """Same in f32 (the host-CPU leg)."""
     import torch

@@ -47,15 +47,16 @@ def gelu_tanh_bf16(src, out):
     return out
 
 
-def new_heads(heads: int, l_total: int, device, valid=None):
-    """bf16 q, k, v buffers [heads, l_total, 128] for qk_norm_rope.  Rows from
-    `valid` on (padding of the joint sequence) are zero, rows before it are left
-    for qk_norm_rope to fill."""
+def new_heads(heads: int, l_total: int, device, valid=None, batch=None):
+    """bf16 q, k, v buffers [heads, l_total, 128] for qk_norm_rope ([batch, heads,
+    l_total, 128] with `batch`).  Rows from `valid` on (padding of the joint
+    sequence) are zero, rows before it are left for qk_norm_rope to fill."""
     import torch
-    bufs = tuple(torch.empty((heads, l_total, HEAD_DIM), dtype=torch.bfloat16, device=device) for _ in range(3))
+    shape = (heads, l_total, HEAD_DIM) if batch is None else (batch, heads, l_total, HEAD_DIM)
+    bufs = tuple(torch.empty(shape, dtype=torch.bfloat16, device=device) for _ in range(3))
     if valid is not None and valid < l_total:
         for t in bufs:
-            t[:, valid:].zero_()
+            t[..., valid:, :].zero_()
     return bufs
 
 

@@ -56,7 +56,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
-from .flux import apply_rope, attention_bf16, aux_stream, gelu_tanh, layer_norm, padded_len, run_guarded, silu
+from .flux import apply_rope, attention_bf16, attention_bf16_batch, aux_stream, gelu_tanh, layer_norm, padded_len, run_guarded, silu
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
 MAX_PERIOD = 10000.0
@@ -442,8 +442,11 @@ class QwenImageStep:
         t_mod_all = P.lin[p + "txt_mod.1"].forward(ts)
         tm = [r.chunk(6, dim=-1) for r in t_mod_all]
         total = lt + L
-        heads_b = [new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total)
-                   for _ in range(B)]
+        # q, k, v of all elements in one [B, H, L, D] buffer each (one batched
+        # attention launch); heads_b[b] are element b's [H, L, D] views
+        hq, hk, hv = new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total,
+                               batch=B)
+        heads_b = [(hq[b], hk[b], hv[b]) for b in range(B)]
         i_att = torch.empty((B * L, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
         t_att = torch.empty((B * lt, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
         # text stream on `aux` as in block(): its modulate, qkv projection and
@@ -461,7 +464,7 @@ class QwenImageStep:
                 qk_norm_rope(ty[b * lt:(b + 1) * lt], H, P.dense[p + "attn.norm_added_q.weight"],
                              P.dense[p + "attn.norm_added_k.weight"], txt_cos, txt_sin, *heads_b[b], 0, cfg.norm_eps)
         if aux is not None:
-            for t in (txt, t_mod_all) + tuple(t for hb in heads_b for t in hb):
+            for t in (txt, t_mod_all, hq, hk, hv):
                 t.record_stream(aux)
         y = P.lin[p + "attn.to_qkv"].forward(self._mod_rows(img, im, 0, 1, B), out_dtype=torch.bfloat16)
         for b in range(B):
@@ -469,20 +472,20 @@ class QwenImageStep:
                          img_cos, img_sin, *heads_b[b], lt, cfg.norm_eps)
         if aux is not None:
             main.wait_stream(aux)
+        drops = []
         for b in range(B):
-            heads = heads_b[b]
-            drop = None
+            drops.append((valid[b], lt) if valid[b] < lt else None)
             if valid[b] < lt:
-                drop = (valid[b], lt)
-                heads[1][:, valid[b]:lt].zero_()
-                heads[2][:, valid[b]:lt].zero_()
-            if self.pad_attention:
-                a = attention_bf16(*heads, valid=total, guard=self._guard, drop=drop)
-            else:   # the guarded rerun: exact attention over the kept keys
-                from .flux import _attention_chunked
-                a = _attention_chunked(*(t[:, :total] for t in heads), drop)
-            t_att[b * lt:(b + 1) * lt] = a[:lt]
-            i_att[b * L:(b + 1) * L] = a[lt:]
+                heads_b[b][1][:, valid[b]:lt].zero_()
+                heads_b[b][2][:, valid[b]:lt].zero_()
+        if self.pad_attention:
+            a = attention_bf16_batch(hq, hk, hv, valid=total, guard=self._guard, drops=drops)
+        else:   # the guarded rerun: exact attention over the kept keys
+            from .flux import _attention_chunked
+            a = [_attention_chunked(*(t[:, :total] for t in heads_b[b]), drops[b]) for b in range(B)]
+        for b in range(B):
+            t_att[b * lt:(b + 1) * lt] = a[b][:lt]
+            i_att[b * L:(b + 1) * L] = a[b][lt:]
         if aux is not None:
             aux.wait_stream(main)
         with on_aux():

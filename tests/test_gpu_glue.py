@@ -128,6 +128,35 @@ def test_padded_attention_matches_reference(valid, padded):
     assert err < 5e-3, err
 
 
+def test_batched_padded_attention_with_dropped_keys():
+    """attention_bf16_batch (one launch over [B, H, L, D], the CFG batch-2 block): element 0
+    with padding only, element 1 with masked keys 30 .. 63 as well (a shorter uncond
+    prompt).  Each element must match f64 attention over its own kept keys, and the guard
+    must hold the largest pad share of both."""
+    from mold_amd.flux import attention_bf16_batch
+    B, H, D, valid, padded, lo, hi = 2, 4, 128, 700, 768, 30, 64
+    print(f"[case] batched padded attention B={B} valid={valid} padded={padded} drop={lo}..{hi}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q, k, v = (torch.randn((B, H, padded, D), device="cuda", generator=g).to(torch.bfloat16) for _ in range(3))
+    k[:, :, valid:] = 0
+    v[:, :, valid:] = 0
+    k[1, :, lo:hi] = 0
+    v[1, :, lo:hi] = 0
+    guard = torch.zeros((), dtype=torch.float32, device="cuda")
+    out = attention_bf16_batch(q, k, v, valid=valid, guard=guard, drops=[None, (lo, hi)])
+    torch.cuda.synchronize()
+    assert out.shape == (B, valid, H * D)
+    keep = [torch.arange(valid), torch.cat([torch.arange(lo), torch.arange(hi, valid)])]
+    for b in range(B):
+        qf = q[b, :, :valid].double().cpu()
+        kf, vf = (t[b, :, keep[b]].double().cpu() for t in (k, v))
+        ref = (torch.softmax(qf @ kf.transpose(1, 2).contiguous() / np.sqrt(D), dim=-1) @ vf)
+        ref = ref.transpose(0, 1).reshape(valid, H * D)
+        err = ((out[b].double().cpu() - ref).norm() / ref.norm()).item()
+        assert err < 5e-3, (b, err)
+    assert 0.0 < float(guard) < 0.5
+
+
 def _anti_aligned(valid, padded, bad_heads, H=4, D=128, seed=7):
     """q, k, v [H, padded, D] bf16 whose heads in `bad_heads` have every valid score
     q.k/sqrt(D) <= -10 (q anti-aligned with all keys), so the zero pad keys hold
