@@ -272,11 +272,14 @@ def test_gemv_q4k_exact_on_q8k_grid(dev, torch, m):
     assert O.rel_l2(y, ref) <= GEMV_TOL, O.rel_l2(y, ref)
 
 
-@pytest.mark.parametrize("n,k,m", [(64 * 37, 3072, 1), (64 * 37, 3072, 3), (320, 4096, 2), (200, 2048, 8)])
+@pytest.mark.parametrize("n,k,m", [(64 * 37, 3072, 1), (64 * 37, 3072, 3), (320, 4096, 2), (200, 2048, 8),
+                                   (64 * 300, 8192, 1), (64 * 300, 8192, 2)])
 def test_gemv_q4k_odd_tile_counts_repeat_bit_identical(dev, torch, n, k, m):
     """Q4_K GEMV at tile counts that are not a multiple of 8 (uneven spread over XCDs)
-    and K up to 4096: repeated calls, with another shape in between, are bit-identical
-    and match candle's algorithm."""
+    and K up to 8192 (at 19200 x 8192 a workgroup owns 75 rows x 32 super-blocks =
+    2400 (row, super-block) pairs: the first 512 issued at once, the next 512 spread
+    over the waves once those landed, the rest loaded one by one): repeated calls,
+    with another shape in between, are bit-identical and match candle's algorithm."""
     t = GgmlDType.Q4_K
     _say(f"gemv odd tiles n={n} k={k} m={m}")
     blocks = _weights(int(t), n, k, seed=n + m)
