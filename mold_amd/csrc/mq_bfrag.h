@@ -88,9 +88,29 @@ __device__ __forceinline__ const uint8_t *chunk_at(const WView &w, int f, int nc
 __device__ __forceinline__ const uint8_t *rec_at(const WView &w, int f, int size, int64_t t, int64_t b, int r) {
   return w.base + w.plane[f] + ((t * w.nb + b) * kRowTile + r) * size;
 }
-__device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
-__device__ __forceinline__ uint32_t ld4(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
-__device__ __forceinline__ uint32_t ld2(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+// Weight loads; NT = nontemporal (for kernels that read each weight byte once:
+// the streaming GEMV; the GEMM re-reads weight tiles through L2 and keeps the
+// default).
+template <bool NT = false>
+__device__ __forceinline__ uint4 ld16(const uint8_t *p) {
+  if constexpr (NT) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+template <bool NT = false>
+__device__ __forceinline__ uint32_t ld4(const uint8_t *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+  else return *reinterpret_cast<const uint32_t *>(p);
+}
+template <bool NT = false>
+__device__ __forceinline__ uint32_t ld2(const uint8_t *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+  else return *reinterpret_cast<const uint16_t *>(p);
+}
 
 // chunk maps shared by several types
 //   super-block types: lane half h holds offsets 16h..16h+15 and 32+16h..32+16h+15
@@ -123,17 +143,18 @@ struct TK45 {
     uint32_t sc03, m03, sc47, m47;
     uint4 qh;
   };
+  template <bool NT = false>
   __device__ static void load_prep(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
-    r.dm = ld4(rec_at(w, 0, 4, t, u, row));
+    r.dm = ld4<NT>(rec_at(w, 0, 4, t, u, row));
     const uint8_t *sp = rec_at(w, 1, 12, t, u, row);
-    r.s0 = ld4(sp);
-    r.s1 = ld4(sp + 4);
-    r.s2 = ld4(sp + 8);
-    if constexpr (kFive) r.qh = ld16(chunk_at(w, 2, 2, t, u, h, row));
+    r.s0 = ld4<NT>(sp);
+    r.s1 = ld4<NT>(sp + 4);
+    r.s2 = ld4<NT>(sp + 8);
+    if constexpr (kFive) r.qh = ld16<NT>(chunk_at(w, 2, 2, t, u, h, row));
   }
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
-    r.q[G] = ld16(chunk_at(w, kQsField, 8, t, u, 2 * G + h, row));
+    r.q[G] = ld16<NT>(chunk_at(w, kQsField, 8, t, u, 2 * G + h, row));
   }
   __device__ static void prep(const Raw &r, Sc &s, int) {
     s.d = h2f((uint16_t)(r.dm & 0xFFFF));
@@ -189,17 +210,18 @@ struct T<Q6_K> {
   struct Sc {
     float ds[8];  // d*sc for (H, p) = index 4H + p
   };
+  template <bool NT = false>
   __device__ static void load_prep(Raw &r, const WView &w, int64_t t, int row, int64_t u, int) {
-    r.sc = ld16(chunk_at(w, 2, 1, t, u, 0, row));
-    r.d = ld2(rec_at(w, 3, 2, t, u, row));
+    r.sc = ld16<NT>(chunk_at(w, 2, 1, t, u, 0, row));
+    r.d = ld2<NT>(rec_at(w, 3, 2, t, u, row));
   }
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
     if constexpr (G & 1) {  // the half's pieces are last used by step 2H+1
       constexpr int H = G >> 1;
-      r.qla[H] = ld16(chunk_at(w, 0, 8, t, u, 4 * H + h, row));
-      r.qlb[H] = ld16(chunk_at(w, 0, 8, t, u, 4 * H + 2 + h, row));
-      r.qh[H] = ld16(chunk_at(w, 1, 4, t, u, 2 * H + h, row));
+      r.qla[H] = ld16<NT>(chunk_at(w, 0, 8, t, u, 4 * H + h, row));
+      r.qlb[H] = ld16<NT>(chunk_at(w, 0, 8, t, u, 4 * H + 2 + h, row));
+      r.qh[H] = ld16<NT>(chunk_at(w, 1, 4, t, u, 2 * H + h, row));
     }
   }
   __device__ static void prep(const Raw &r, Sc &s, int h) {
@@ -242,17 +264,18 @@ struct T<Q3_K> {
     float dl[8];  // d*(sc-32) for (H, p) = 4H + p
     uint4 hm;
   };
+  template <bool NT = false>
   __device__ static void load_prep(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
-    r.hm = ld16(chunk_at(w, 0, 2, t, u, h, row));
+    r.hm = ld16<NT>(chunk_at(w, 0, 2, t, u, h, row));
     const uint8_t *sp = rec_at(w, 2, 12, t, u, row);
-    r.s0 = ld4(sp);
-    r.s1 = ld4(sp + 4);
-    r.s2 = ld4(sp + 8);
-    r.d = ld2(rec_at(w, 3, 2, t, u, row));
+    r.s0 = ld4<NT>(sp);
+    r.s1 = ld4<NT>(sp + 4);
+    r.s2 = ld4<NT>(sp + 8);
+    r.d = ld2<NT>(rec_at(w, 3, 2, t, u, row));
   }
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
-    if constexpr (G & 1) r.qs[G >> 1] = ld16(chunk_at(w, 1, 4, t, u, 2 * (G >> 1) + h, row));
+    if constexpr (G & 1) r.qs[G >> 1] = ld16<NT>(chunk_at(w, 1, 4, t, u, 2 * (G >> 1) + h, row));
   }
   __device__ static void prep(const Raw &r, Sc &s, int h) {
     const float d = h2f((uint16_t)r.d);
@@ -296,13 +319,14 @@ struct T<Q2_K> {
   struct Sc {
     float dl[8], ml[8];
   };
+  template <bool NT = false>
   __device__ static void load_prep(Raw &r, const WView &w, int64_t t, int row, int64_t u, int) {
-    r.sc = ld16(chunk_at(w, 0, 1, t, u, 0, row));
-    r.dm = ld4(rec_at(w, 2, 4, t, u, row));
+    r.sc = ld16<NT>(chunk_at(w, 0, 1, t, u, 0, row));
+    r.dm = ld4<NT>(rec_at(w, 2, 4, t, u, row));
   }
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
-    if constexpr (G & 1) r.qs[G >> 1] = ld16(chunk_at(w, 1, 4, t, u, 2 * (G >> 1) + h, row));
+    if constexpr (G & 1) r.qs[G >> 1] = ld16<NT>(chunk_at(w, 1, 4, t, u, 2 * (G >> 1) + h, row));
   }
   __device__ static void prep(const Raw &r, Sc &s, int h) {
     const float d = h2f((uint16_t)(r.dm & 0xFFFF)), dmin = h2f((uint16_t)(r.dm >> 16));
@@ -345,13 +369,14 @@ struct T32 {
     uint32_t d[4], qh[4];
   };
   struct Sc {};
+  template <bool NT = false>
   __device__ static void load_prep(Raw &, const WView &, int64_t, int, int64_t, int) {}
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
     const int64_t b = 8 * u + 2 * G + h;
-    r.q[G] = ld16(chunk_at(w, kQsField, 1, t, b, 0, row));
-    r.d[G] = kMin ? ld4(rec_at(w, 0, 4, t, b, row)) : ld2(rec_at(w, 0, 2, t, b, row));
-    if constexpr (kFive) r.qh[G] = ld4(rec_at(w, 1, 4, t, b, row));
+    r.q[G] = ld16<NT>(chunk_at(w, kQsField, 1, t, b, 0, row));
+    r.d[G] = kMin ? ld4<NT>(rec_at(w, 0, 4, t, b, row)) : ld2<NT>(rec_at(w, 0, 2, t, b, row));
+    if constexpr (kFive) r.qh[G] = ld4<NT>(rec_at(w, 1, 4, t, b, row));
   }
   __device__ static void prep(const Raw &, Sc &, int) {}
   // bits sh..sh+3 of qh spread to bit 4 of bytes 0..3
@@ -397,13 +422,14 @@ struct T<Q8_0> {
     uint32_t d[2];
   };
   struct Sc {};
+  template <bool NT = false>
   __device__ static void load_prep(Raw &, const WView &, int64_t, int, int64_t, int) {}
-  template <int G>
+  template <int G, bool NT = false>
   __device__ static void reload(Raw &r, const WView &w, int64_t t, int row, int64_t u, int h) {
     const int64_t b = 4 * u + 2 * G + h;
-    r.q[G][0] = ld16(chunk_at(w, 1, 2, t, b, 0, row));
-    r.q[G][1] = ld16(chunk_at(w, 1, 2, t, b, 1, row));
-    r.d[G] = ld2(rec_at(w, 0, 2, t, b, row));
+    r.q[G][0] = ld16<NT>(chunk_at(w, 1, 2, t, b, 0, row));
+    r.q[G][1] = ld16<NT>(chunk_at(w, 1, 2, t, b, 1, row));
+    r.d[G] = ld2<NT>(rec_at(w, 0, 2, t, b, row));
   }
   __device__ static void prep(const Raw &, Sc &, int) {}
   template <int G, int S, typename O = bf16x8>
