@@ -211,6 +211,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
 constexpr int kFM = kGemmTileM, kFN = kGemmTileN, kFK = 64;
 constexpr int kFastThreads = 256;
 constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
+constexpr int MQ_ACT_GELU_ = 1;  // mq_act MQ_ACT_GELU_TANH (the only other value)
 
 // 16 bytes per lane from sbase + voff straight into LDS: lane i of the wave
 // writes LDS bytes lds + 16 i .. + 15 (global_load_lds_dwordx4, saddr form).
@@ -408,11 +409,20 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     }
     return;
   } else {
-    if (m0 + kFM <= m && c0 + 32 <= n && act == MQ_ACT_NONE_) {
+    if (m0 + kFM <= m && c0 + 32 <= n) {
+      // whole tile: no row checks, the activation chosen once
+      if (act == MQ_ACT_NONE_) {
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
+        for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
+          for (int e = 0; e < 16; ++e) store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
+      } else {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, act_out<OUT>(acc[mb][e] + bv, MQ_ACT_GELU_));
+      }
       return;
     }
     if (!colok) return;
