@@ -388,6 +388,25 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     // rows past m and columns past n are neither read nor written
     const float g = colok ? gate[col] : 0.f;
     float r[2][16];
+    if (m0 + kFM <= m && c0 + 32 <= n && act == MQ_ACT_NONE_) {
+      // whole tile, no activation (every gated linear of the block graphs):
+      // no bounds checks
+      auto load_full = [&](int mb, float *dst) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dst[e] = yc[(mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy];
+      };
+      load_full(0, r[0]);
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        if (mb + 1 < 8) load_full(mb + 1, r[(mb + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          yc[(mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy] = __builtin_fmaf(g, acc[mb][e] + bv, r[mb & 1][e]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
     auto load_block = [&](int mb, float *dst) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
