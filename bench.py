@@ -24,6 +24,9 @@ Also on the same JSON line:
   * "config3_mlp": BASELINE config 3, the MLP chain fc1 (3072->12288, GELU-tanh
     epilogue, bf16 out) then fc2 (12288->3072, f32 out) on f32 x [4608, 3072],
     for Q4_K, Q4_0 and Q6_K weights;
+  * "tp8_shards": one GPU's share of FLUX's linear1 (column split, N/8) and linear2
+    (row split, largest whole-super-block share, gated) under 8-way tensor
+    parallelism, at the real shapes (no collective is run);
   * "dequant": QTensor::dequantize of a Q4_K 18432x3072 weight to f32 and to
     bf16, in GB/s of algorithmic bytes (GGUF blocks read + dense out written);
   * "gemv": the skinny-M Q4_K modulation GEMVs (config 2, M in {1, 2, 4},
@@ -204,6 +207,41 @@ def bench_config1(dev, args):
             "gemm_kernel_frac": round(flop / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "what": "f32 x staged to bf16 + fused Q8_0 GEMM (ms, tflops, frac); the GEMM alone on bf16 x "
                     "(gemm_kernel_*)"}
+
+
+def bench_tp8_shards(dev, args):
+    """One GPU's share of FLUX's single-block linears under 8-way tensor parallelism, at its real
+    shape: linear1 column-split (N/8 = 2688 output features, no exchange) and linear2 row-split.
+    linear2's K = 15360 is 60 Q4_K super-blocks, which 8 GPUs cannot split evenly (K/8 = 1920 is
+    not a whole number of 256-element blocks): the shares are 8 and 7 super-blocks, and the
+    largest (K = 2048) is timed, as the gated update it would feed before the all-reduce."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    from mold_amd.quantized import Linear
+    m = 4608
+    g = torch.Generator(device="cuda").manual_seed(40)
+    out = []
+    for name, n, k, gated in (("linear1 column shard", 21504 // 8, 3072, False),
+                              ("linear2 row shard (largest)", 3072, 2048, True)):
+        log(f"tp8 shard: {name} {m}x{k}->{n}")
+        qt = make_weight(dev, GgmlDType.Q4_K, n, k, seed=41 + len(out))
+        x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+        y = torch.zeros((m, n), device="cuda")
+        if gated:
+            lin = Linear(qt)
+            gate = torch.randn(n, device="cuda", generator=g)
+            fn = lambda: lin.gated_add(x, gate, y)
+        else:
+            mm = mold_amd.QMatMul(qt)
+            fn = lambda: mm.forward(x, out=y)
+        flop = 2.0 * m * n * k
+        _, ms = timed(fn, max(50, args.steps), 5, prewarm_s=0.2)
+        out.append({"linear": name, "m": m, "n": n, "k": k, "gated": gated, "ms": round(ms, 4),
+                    "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                    "frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+        del qt, x, y
+    return out
 
 
 def bench_config3(dev, args):
@@ -798,6 +836,7 @@ def main():
     if not args.no_extra:
         extra["config1_q8_0"] = bench_config1(dev, args)
         extra["config3_mlp"] = bench_config3(dev, args)
+        extra["tp8_shards"] = bench_tp8_shards(dev, args)
         extra["dequant"] = bench_dequant(dev, args)
         extra["dense_bf16_ceiling"] = bench_dense_ceiling(args)
         extra["upload"] = bench_upload(dev, args)

@@ -100,13 +100,21 @@ def test_config3_mlp_chain(dev, torch, tname):
     assert e1 <= TOL and e2 <= TOL and e3 <= TOL
 
 
-@pytest.mark.parametrize("shape", ["qkv_Q3_K", "fc1_Q2_K_gelu_bf16", "fc2_Q2_K_gated", "out_Q4_K_gated"])
+@pytest.mark.parametrize("shape", ["qkv_Q3_K", "fc1_Q2_K_gelu_bf16", "fc2_Q2_K_gated", "out_Q4_K_gated",
+                                   "tp8_linear1_shard", "tp8_linear2_shard_gated"])
 def test_config5_lowbit_gemms(dev, torch, shape):
-    """Qwen-Image block linears at M = 6889 (27 row panels, the last one 233 rows)."""
+    """Qwen-Image block linears at M = 6889 (27 row panels, the last one 233 rows), and one
+    GPU's share of FLUX's single-block linears under 8-way tensor parallelism at M = 4608:
+    linear1 column-split (N = 21504 / 8) and linear2's largest row share (K = 2048, 8 of its
+    60 super-blocks), as timed by bench.py's tp8_shards leg."""
     m, h, mlp = 6889, 3072, 12288
     spec = {"qkv_Q3_K": ("Q3_K", 3 * h, h, "bf16"), "fc1_Q2_K_gelu_bf16": ("Q2_K", mlp, h, "gelu_bf16"),
-            "fc2_Q2_K_gated": ("Q2_K", h, mlp, "gated"), "out_Q4_K_gated": ("Q4_K", h, h, "gated")}[shape]
+            "fc2_Q2_K_gated": ("Q2_K", h, mlp, "gated"), "out_Q4_K_gated": ("Q4_K", h, h, "gated"),
+            "tp8_linear1_shard": ("Q4_K", 21504 // 8, h, "bf16"),
+            "tp8_linear2_shard_gated": ("Q4_K", h, 2048, "gated")}[shape]
     tname, n, k, mode = spec
+    if shape.startswith("tp8"):
+        m = 4608
     t = GgmlDType[tname]
     _say(f"config 5 {shape} m={m} n={n} k={k}")
     blocks = _weights(t, n, k, 50 + n + k)
