@@ -170,7 +170,7 @@ def bench_gemm(dev, args):
     log(f"pre-warm 1 s, warmup {args.warmup}, timing {args.steps} steps")
     wall_ms, kern_ms = timed(lambda: mm.forward(xb, out=y), args.steps, args.warmup, prewarm_s=1.0)
     assert torch.isfinite(y).all().item(), "non-finite GEMM output"
-    f32_wall, f32_ev = timed(lambda: mm.forward(x, out=y), max(20, args.steps // 4), 3)
+    f32_wall, f32_ev = timed(lambda: mm.forward(x, out=y), max(20, args.steps // 4), 3, prewarm_s=1.0)
     res = {
         "ms_per_step": wall_ms,
         "tflops": flop / (wall_ms * 1e-3) / 1e12,
