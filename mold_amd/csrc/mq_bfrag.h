@@ -61,13 +61,27 @@ __device__ __forceinline__ O fma8(uint32_t w0, uint32_t w1, float a, float b) {
   v[5] = __builtin_fmaf(ub<1>(w1), a, b);
   v[6] = __builtin_fmaf(ub<2>(w1), a, b);
   v[7] = __builtin_fmaf(ub<3>(w1), a, b);
-  O r;
+  if constexpr (__is_same(O, f32x8)) {
+    O r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if constexpr (__is_same(O, f32x8)) r[i] = v[i];
-    else r[i] = (__bf16)v[i];
+    for (int i = 0; i < 8; ++i) r[i] = v[i];
+    return r;
+  } else {
+    // one v_cvt_pk_bf16_f32 per adjacent pair, each into its own 32-bit lane
+    // of the fragment (element-wise conversions were sometimes paired with a
+    // zero register and reassembled with v_perm / v_alignbit)
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x2 p = __builtin_convertvector((f32x2){v[2 * j], v[2 * j + 1]}, bf16x2);
+      __builtin_memcpy(&u[j], &p, 4);
+    }
+    O r;
+    __builtin_memcpy(&r, u, 16);
+    return r;
   }
-  return r;
 }
 
 // Words (x, y) for even slices, (z, w) for odd ones.
