@@ -49,14 +49,18 @@ Also on the same JSON line:
     4096 image + 512 text tokens, every linear Q4_K except the bf16 img_in),
     built by mold_amd.flux on these quantized linears, in ms per step, with
     its own host-CPU baseline (stems, one double block, one single block and
-    the final layer on the CPU, extrapolated x19 / x38 and labelled so);
+    the final layer on the CPU, extrapolated x19 / x38 and labelled so); its
+    "modulation_stack" is the step's 77 adaLN modulation linears (one
+    StackedLinear, 1,056,768 x 3072 Q4_K) as the one GEMV the step runs, timed
+    alone, in GB/s against the HBM peak;
   * "qwen_step": one Qwen-Image-shaped denoising-step forward at 1328^2
     (60 dual-stream blocks, 6889 image + 256 text
     tokens, q/k/v Q3_K, MLP Q2_K, out-projections and modulation Q4_K), built
     by mold_amd.qwen_image, in ms per step, with a host-CPU baseline (stems,
     block 0 and the output layer on the CPU, extrapolated x60), and the
     batch-2 classifier-free-guidance forward (cond + a shorter, masked uncond
-    prompt) in ms ("cfg_batch2_ms");
+    prompt) in ms ("cfg_batch2_ms"), and its 121 modulation linears' stacked
+    GEMV (2,217,984 x 3072 Q4_K) at M = 1 and 2 ("modulation_stack");
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated in C under
     oracle/, timed on a bounded row sample of the headline workload on this
@@ -508,6 +512,40 @@ def bench_gemv(dev, args):
     return out
 
 
+def bench_stack(stack, ms_list, args):
+    """The step's stacked modulation GEMV alone (StackedLinear: every block's
+    adaLN modulation weight in one Q4_K tensor, one launch), captured in a HIP
+    graph and replayed; its weight is far larger than the Infinity Cache, so
+    every replay streams it from HBM."""
+    import torch
+    lin = stack.linear
+    n, k = lin.matmul.w.shape
+    wbytes = lin.matmul.w.storage_size_in_bytes()
+    out = []
+    for m in ms_list:
+        x = torch.randn((m, k), device="cuda", generator=torch.Generator(device="cuda").manual_seed(m))
+        y = torch.empty((m, n), device="cuda")
+
+        def run():
+            lin.matmul.forward(x, bias=lin.bias, out=y)
+        run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run()
+        graph.replay()
+        torch.cuda.synchronize()
+        _, ms = timed(graph.replay, max(10, args.steps), 2, prewarm_s=0.1)
+        nbytes = wbytes + 4 * m * k + 4 * n + 4 * m * n
+        out.append({"m": m, "n": n, "k": k, "parts": len(stack.names), "us": round(ms * 1e3, 2), "bytes": nbytes,
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+        log(f"  stacked modulation GEMV m={m}: {len(stack.names)} linears, {n} rows, {ms*1e3:.1f} us, "
+            f"{out[-1]['gbs']:.0f} GB/s ({out[-1]['frac']:.3f} of peak)")
+        del graph
+    return out
+
+
 def bench_flux(dev, args):
     """One FLUX.1-dev-shaped Q4_K step at 1024^2, eager, ms per step."""
     import torch
@@ -536,7 +574,9 @@ def bench_flux(dev, args):
     lin, attn = F.step_flop(cfg, 4096, 512)
     ms = sorted(times)[len(times) // 2]
     log(f"  step {ms:.2f} ms (median of {n}), attention backend {F.ATTENTION_BACKEND['name']}")
+    stack = bench_stack(step._mod_stack, (1,), args)
     res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
+           "modulation_stack": stack,
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
            "weight_bytes": params.quantized_bytes(), "attention": F.ATTENTION_BACKEND["name"],
@@ -595,7 +635,9 @@ def bench_qwen(dev, args):
     lin, attn = Q.step_flop(cfg, l_img, 256)
     ms = sorted(times)[len(times) // 2]
     log(f"  step {ms:.2f} ms (median of {n}), attention backend {ATTENTION_BACKEND['name']}")
+    stack = bench_stack(step._mod_stack, (1, 2), args)
     res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
+           "modulation_stack": stack,
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
            "cfg_batch2_ms": round(bms, 3), "cfg_batch2_steps_timed": len(btimes),

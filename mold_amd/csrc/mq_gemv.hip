@@ -182,7 +182,7 @@ struct Q4kPair {
   uint32_t dm, s0, s1, s2;
 };
 
-template <int M, typename XT, typename OUT>
+template <int M, typename XT, typename OUT, bool kOne>
 __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     WView w, int64_t n, int64_t nrows_mem, int nb, int rows, const XT *__restrict__ x, int64_t ldx,
     OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act) {
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
       }
     }
   }
-  Q4kPair slot[2];
+  Q4kPair slot[kOne ? 1 : 2];
   load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
   asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
   __syncthreads();
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     int S[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) S[m] = 0;
-    if constexpr (M <= 2) {
+    if constexpr (M <= 2 && !kOne) {
       // steps s = (g, m) in order g-major: chunks 2g and 2g+1 (32 bytes) hold
       // elements 64g + 0..31 in their low nibbles (sub-block 2g) and 64g +
       // 32..63 in their high nibbles (sub-block 2g+1), each in byte order; one
@@ -433,17 +433,23 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   // every dot would run after it; in two waves the first pairs land at about
   // the middle and only the second pairs' dots follow the stream.  Pairs past
   // 1024 (K beyond 2 * 512 pairs' worth) load as they go.
-  const int n2 = (npairs < 2 * kQ4kThreads ? npairs : 2 * kQ4kThreads) - kQ4kThreads;
-  const int per = n2 > 0 ? (n2 + kWaves - 1) / kWaves : 0;
-  const int p1 = kQ4kThreads + per * wave + lane;
-  const bool has1 = lane < per && p1 < npairs;
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first pair has landed
-  if (has1) load_pair(p1, slot[1]);
-  dot_pair(tid, slot[0]);
-  if (has1) dot_pair(p1, slot[1]);
-  for (int p = tid + 2 * kQ4kThreads; p < npairs; p += kQ4kThreads) {
-    load_pair(p, slot[0]);
-    dot_pair(p, slot[0]);
+  if constexpr (kOne) {
+    // every pair of the workgroup is thread tid's slot 0
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    dot_pair(tid, slot[0]);
+  } else {
+    const int n2 = (npairs < 2 * kQ4kThreads ? npairs : 2 * kQ4kThreads) - kQ4kThreads;
+    const int per = n2 > 0 ? (n2 + kWaves - 1) / kWaves : 0;
+    const int p1 = kQ4kThreads + per * wave + lane;
+    const bool has1 = lane < per && p1 < npairs;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first pair has landed
+    if (has1) load_pair(p1, slot[1]);
+    dot_pair(tid, slot[0]);
+    if (has1) dot_pair(p1, slot[1]);
+    for (int p = tid + 2 * kQ4kThreads; p < npairs; p += kQ4kThreads) {
+      load_pair(p, slot[0]);
+      dot_pair(p, slot[0]);
+    }
   }
   __syncthreads();
 
@@ -639,16 +645,25 @@ static int q4k_rows(int64_t n, int64_t nb, int64_t m, int cus) {
   return (int)rows;
 }
 
+// When a workgroup has at most one pair per thread, the single-slot instance
+// runs it (no second register slot, no Q8_K prefetch: far fewer VGPRs).
+static bool q4k_one_slot(int64_t nb, int rows) { return (int64_t)rows * nb <= kQ4kThreads; }
+
 template <int M, typename XT, typename OUT>
 static void launch_gemv_q4k(const WView &w, int64_t n, int64_t k, const XT *x, int64_t ldx, OUT *y, int64_t ldy,
                             const float *bias, int act, int cus, hipStream_t stream) {
   const int64_t nb = k / 256;
   const int rows = q4k_rows(n, nb, M, cus);
+  const bool one = q4k_one_slot(nb, rows);
   const int64_t wgs = (n + rows - 1) / rows;
   const int64_t nrows_mem = ((n + kRowTile - 1) / kRowTile) * kRowTile;
-  hipLaunchKernelGGL((gemv_q4k_kernel<M, XT, OUT>), dim3((unsigned)wgs), dim3(kQ4kThreads),
-                     q4k_lds_bytes(nb, M, rows, (int)sizeof(XT)), stream, w, n, nrows_mem, (int)nb, rows, x, ldx, y,
-                     ldy, bias, act);
+  const size_t lds = q4k_lds_bytes(nb, M, rows, (int)sizeof(XT));
+  if (one)
+    hipLaunchKernelGGL((gemv_q4k_kernel<M, XT, OUT, true>), dim3((unsigned)wgs), dim3(kQ4kThreads), lds, stream, w,
+                       n, nrows_mem, (int)nb, rows, x, ldx, y, ldy, bias, act);
+  else
+    hipLaunchKernelGGL((gemv_q4k_kernel<M, XT, OUT, false>), dim3((unsigned)wgs), dim3(kQ4kThreads), lds, stream, w,
+                       n, nrows_mem, (int)nb, rows, x, ldx, y, ldy, bias, act);
 }
 
 static int pick_ksplit(int64_t ntiles, int64_t k) {

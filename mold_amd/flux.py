@@ -29,8 +29,11 @@ q/k norm + RoPE + head split run as libmoldq's fused row passes
 each gated residual update x + gate * linear(h) is the GEMM's epilogue
 (Linear.gated_add, updating x in place); a tensor whose only consumer is a quantized GEMM is produced directly in bf16
 (the GEMM rounds its input to bf16 with round-to-nearest-even either way, so
-the f32 -> bf16 staging pass disappears); and attention runs in bf16 with f32
-softmax accumulation (PyTorch's fused attention) rather than as three f32 ops.
+the f32 -> bf16 staging pass disappears); attention runs in bf16 with f32
+softmax accumulation (PyTorch's fused attention) rather than as three f32 ops;
+and every block's adaLN modulation linear, which reads the same silu(vec),
+runs in one GEMV over the stacked modulation weights (StackedLinear) at the
+start of the forward, with outputs identical to the per-block linears.
 
 Weights are synthetic (no checkpoint exists here): every linear weight is
 N(0, 0.02^2) quantized on the GPU to the configured GGUF type, biases are f32
@@ -430,6 +433,11 @@ class FluxStep:
         self.bf16_projections = True
         self.pad_attention = True
         self._guard = None
+        # every modulation linear reads silu(vec): on the GPU they run as one
+        # stacked GEMV per forward (StackedLinear, built on first use)
+        self.stack_modulations = True
+        self._mod_stack = None
+        self._mods = None
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused) for the modulate and the
@@ -441,8 +449,25 @@ class FluxStep:
 
     # -- pieces, each following offload.rs
     def _mod(self, name, vec, n):
-        y = self.p.lin[name].forward(silu(vec))
+        y = self._mods[name] if self._mods is not None else self.p.lin[name].forward(silu(vec))
         return y.chunk(n, dim=-1)
+
+    def modulation_names(self):
+        """The modulation linears in run order (each reads silu(vec))."""
+        cfg = self.cfg
+        names = []
+        for i in range(cfg.depth):
+            names += [f"double_blocks.{i}.img_mod.lin", f"double_blocks.{i}.txt_mod.lin"]
+        names += [f"single_blocks.{i}.modulation.lin" for i in range(cfg.depth_single_blocks)]
+        return names + ["final_layer.adaLN_modulation.1"]
+
+    def _stacked_mods(self, vec):
+        from .quantized import StackedLinear
+        if self._mod_stack is None:
+            lin = self.p.lin[self.modulation_names()[0]]
+            self._mod_stack = StackedLinear(lin.matmul.w.device,
+                                            [(nm, self.p.lin[nm]) for nm in self.modulation_names()])
+        return self._mod_stack.forward(silu(vec))
 
     def _qkv(self, prefix, x, qn, kn):
         cfg = self.cfg
@@ -604,7 +629,7 @@ class FluxStep:
         return img_h, txt_h, vec
 
     def final_layer(self, x, vec):
-        shift, scale = self.p.lin["final_layer.adaLN_modulation.1"].forward(silu(vec)).chunk(2, dim=-1)
+        shift, scale = self._mod("final_layer.adaLN_modulation.1", vec, 2)
         import torch
         return self.p.lin["final_layer.linear"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
 
@@ -625,12 +650,17 @@ class FluxStep:
         ns = self.cfg.depth_single_blocks if blocks is None else blocks[1]
         cos, sin = self.rope(img_ids, txt_ids)
         img_h, txt_h, vec = self.stems(img, txt, t, guidance, y)
-        for i in range(nd):
-            img_h, txt_h = self.double_block(i, img_h, txt_h, vec, cos, sin)
-        x = torch.cat([txt_h, img_h], dim=0)
-        for i in range(ns):
-            x = self.single_block(i, x, vec, cos, sin)
-        return self.final_layer(x[txt_h.shape[0]:], vec)
+        stacked = self.stack_modulations and vec.is_cuda and blocks is None
+        self._mods = self._stacked_mods(vec) if stacked else None
+        try:
+            for i in range(nd):
+                img_h, txt_h = self.double_block(i, img_h, txt_h, vec, cos, sin)
+            x = torch.cat([txt_h, img_h], dim=0)
+            for i in range(ns):
+                x = self.single_block(i, x, vec, cos, sin)
+            return self.final_layer(x[txt_h.shape[0]:], vec)
+        finally:
+            self._mods = None
 
 
 def make_inputs(cfg: FluxConfig, height: int = 1024, width: int = 1024, txt_len: int = 512,

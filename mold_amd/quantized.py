@@ -18,7 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import enum
-from typing import Optional, Sequence
+from typing import Dict, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -291,5 +291,49 @@ class Linear:
                                                b.data_ptr() if b is not None else None, g.data_ptr(),
                                                _stream_ptr(stream)))
         return residual
+
+    __call__ = forward
+
+
+class StackedLinear:
+    """Quantized linears that read the same input, stacked by rows into one
+    resident weight so that one GEMV / GEMM computes all of them.
+
+    mold's DiT blocks each project the same conditioning vector (FLUX's
+    `vec`, Qwen-Image's `temb`) through their own adaLN modulation linear
+    (flux/offload.rs:143-156 and :282-283, qwen_image/quantized_transformer.rs:869-881);
+    stacked, a step's modulations are one launch streaming every modulation
+    weight once.  Each output row is computed by the same per-row arithmetic
+    as in the part's own forward, so the outputs are identical.  The stacked
+    weight is a byte copy of the parts' GGUF blocks (same type and k); the
+    parts stay usable on their own."""
+
+    def __init__(self, device: Device, parts: Sequence[Tuple[str, Linear]]):
+        torch = _torch()
+        if not parts:
+            raise ValueError("StackedLinear needs at least one part")
+        w0 = parts[0][1].matmul.w
+        dtype, k = w0.dtype(), w0.shape[1]
+        self.names, self.offsets = [], {}
+        blocks, biases, row = [], [], 0
+        for name, lin in parts:
+            w = lin.matmul.w
+            if w.dtype() != dtype or w.shape[1] != k:
+                raise ValueError(f"StackedLinear: {name} is {w.dtype().name} [{w.shape[0]}, {w.shape[1]}], "
+                                 f"the stack {dtype.name} with k = {k}")
+            n = w.shape[0]
+            blocks.append(w.data())
+            biases.append(lin.bias if lin.bias is not None
+                          else torch.zeros((n,), dtype=torch.float32, device=f"cuda:{device.ordinal}"))
+            self.names.append(name)
+            self.offsets[name] = (row, n)
+            row += n
+        qt = QTensor.from_blocks(device, dtype, (row, k), np.concatenate(blocks))
+        self.linear = Linear(qt, torch.cat([b.reshape(-1).float() for b in biases]).contiguous())
+
+    def forward(self, x, out_dtype=None, stream=None) -> Dict[str, object]:
+        """{part name: its output [..., n_part]} (column views of one result)."""
+        y = self.linear.forward(x, out_dtype=out_dtype, stream=stream)
+        return {name: y[..., r0:r0 + n] for name, (r0, n) in self.offsets.items()}
 
     __call__ = forward

@@ -40,6 +40,10 @@ Layout choices made here (the graph's values are unchanged by them):
     into the joint [heads, L, 128] bf16 buffers attention reads, and each
     gated residual update x + gate * linear(h) is the GEMM's epilogue
     (Linear.gated_add, updating x in place).
+  * Every block's img_mod.1 / txt_mod.1 and the output layer's norm_out.linear
+    read the same silu(temb): on the GPU they run as one GEMV (one GEMM row
+    per batch element) over their weights stacked by rows (StackedLinear) at
+    the start of the forward, with outputs identical to the separate linears.
   * The text attention mask is all ones for an unpadded prompt, which makes the
     mask a no-op (:813-815 add 0 to every score), so none is applied.
 
@@ -235,6 +239,32 @@ class QwenImageStep:
         self.bf16_projections = True
         self.pad_attention = True
         self._guard = None
+        self.stack_modulations = True
+        self._mod_stack = None
+        self._mods = None
+
+    def modulation_names(self):
+        """The linears that read silu(temb), in run order."""
+        names = []
+        for i in range(self.cfg.num_layers):
+            names += [f"transformer_blocks.{i}.img_mod.1", f"transformer_blocks.{i}.txt_mod.1"]
+        return names + ["norm_out.linear"]
+
+    def _start_mods(self, ts, blocks):
+        """Run the stacked modulation GEMV for this forward (GPU, all blocks)."""
+        from .quantized import StackedLinear
+        self._mods = None
+        if not (self.stack_modulations and ts.is_cuda and blocks is None):
+            return
+        if self._mod_stack is None:
+            names = self.modulation_names()
+            self._mod_stack = StackedLinear(self.p.lin[names[0]].matmul.w.device,
+                                            [(nm, self.p.lin[nm]) for nm in names])
+        self._mods = self._mod_stack.forward(ts)
+
+    def _modf(self, name, ts):
+        """Output of modulation linear `name` on ts = silu(temb)."""
+        return self._mods[name] if self._mods is not None else self.p.lin[name].forward(ts)
 
     def _fused(self, x) -> bool:
         """Use libmoldq's fused row passes (mold_amd.fused): on the GPU with bf16 GEMM inputs."""
@@ -291,8 +321,8 @@ class QwenImageStep:
         import torch
         p = f"transformer_blocks.{i}."
         img_cos, img_sin, txt_cos, txt_sin = rope
-        i_mod_all = self.p.lin[p + "img_mod.1"].forward(temb_silu)
-        t_mod_all = self.p.lin[p + "txt_mod.1"].forward(temb_silu)
+        i_mod_all = self._modf(p + "img_mod.1", temb_silu)
+        t_mod_all = self._modf(p + "txt_mod.1", temb_silu)
         i_mod, t_mod = i_mod_all.chunk(6, dim=-1), t_mod_all.chunk(6, dim=-1)
         aux = self._aux(img)
         lt = txt.shape[0]
@@ -380,7 +410,7 @@ class QwenImageStep:
     def output_layer(self, x, temb):
         """OutputLayer.forward (:977-989): chunk 0 is scale, chunk 1 shift."""
         import torch
-        scale, shift = self.p.lin["norm_out.linear"].forward(silu(temb)).chunk(2, dim=-1)
+        scale, shift = self._modf("norm_out.linear", silu(temb)).chunk(2, dim=-1)
         return self.p.lin["proj_out"].forward(self._modulate(x, shift, scale), out_dtype=torch.float32)
 
     def forward(self, img, txt, t, grid: Tuple[int, int], blocks: Optional[int] = None):
@@ -438,8 +468,8 @@ class QwenImageStep:
         img_cos, img_sin, txt_cos, txt_sin = rope
         L, lt = img.shape[0] // B, txt.shape[0] // B
         H = cfg.num_attention_heads
-        im = [r.chunk(6, dim=-1) for r in P.lin[p + "img_mod.1"].forward(ts)]      # M = B GEMV
-        t_mod_all = P.lin[p + "txt_mod.1"].forward(ts)
+        im = [r.chunk(6, dim=-1) for r in self._modf(p + "img_mod.1", ts)]      # M = B GEMV
+        t_mod_all = self._modf(p + "txt_mod.1", ts)
         tm = [r.chunk(6, dim=-1) for r in t_mod_all]
         total = lt + L
         # q, k, v of all elements in one [B, H, L, D] buffer each (one batched
@@ -512,9 +542,13 @@ class QwenImageStep:
         rope = rope_tables(cfg, 1, grid[0], grid[1], lt, img.device)
         img_h, txt_h, temb = self.stems(img.reshape(B * L, c), txt.reshape(B * lt, -1), t)
         ts = silu(temb)                                   # [B, h]
-        for i in range(nb):
-            img_h, txt_h = self.block_batched(i, img_h, txt_h, ts, rope, B, valid)
-        om = [r.chunk(2, dim=-1) for r in self.p.lin["norm_out.linear"].forward(ts)]   # (scale, shift)
+        self._start_mods(ts, blocks)
+        try:
+            for i in range(nb):
+                img_h, txt_h = self.block_batched(i, img_h, txt_h, ts, rope, B, valid)
+            om = [r.chunk(2, dim=-1) for r in self._modf("norm_out.linear", ts)]   # (scale, shift)
+        finally:
+            self._mods = None
         x = self._mod_rows(img_h, [(o[1], o[0]) for o in om], 0, 1, B)
         return self.p.lin["proj_out"].forward(x, out_dtype=torch.float32).reshape(B, L, -1)
 
@@ -524,9 +558,13 @@ class QwenImageStep:
         rope = rope_tables(cfg, 1, grid[0], grid[1], txt.shape[0], img.device)
         img_h, txt_h, temb = self.stems(img, txt, t)
         ts = silu(temb)
-        for i in range(nb):
-            img_h, txt_h = self.block(i, img_h, txt_h, ts, rope)
-        return self.output_layer(img_h, temb)
+        self._start_mods(ts, blocks)
+        try:
+            for i in range(nb):
+                img_h, txt_h = self.block(i, img_h, txt_h, ts, rope)
+            return self.output_layer(img_h, temb)
+        finally:
+            self._mods = None
 
 
 def make_inputs(cfg: QwenConfig, height: int = 1328, width: int = 1328, txt_len: int = 256,

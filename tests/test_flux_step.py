@@ -191,8 +191,15 @@ def test_flux_step_tiny_matches_dequantized_reference():
     dev = mold_amd.Device(0)
     params = F.FluxParams.random(cfg, dev, seed=6)
     inp = F.make_inputs(cfg, height=256, width=256, txt_len=32, device="cuda", seed=6)
-    out = F.FluxStep(params).forward(**inp)
+    step = F.FluxStep(params)
+    out = step.forward(**inp)
+    # the modulations as one stacked GEMV (default) or one GEMV per block: same values
+    sep = F.FluxStep(params)
+    sep.stack_modulations = False
+    out_sep = sep.forward(**inp)
     torch.cuda.synchronize()
+    assert step._mod_stack is not None and sep._mod_stack is None
+    assert torch.equal(out, out_sep)
     W = {}
     for name, l in params.lin.items():
         qt = l.matmul.w

@@ -593,6 +593,39 @@ def test_full_config2_modulation_gemv(dev, torch, n, m):
     _gemv_check(t, x, y, blocks, n, k)
 
 
+@pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q8_0], ids=lambda t: t.name)
+@pytest.mark.parametrize("m", [1, 2])
+def test_stacked_linear_matches_separate_linears(dev, torch, t, m):
+    """A step's modulation linears stacked by rows (FLUX's double-block, single-block
+    and final-layer shapes): every part's columns of the one stacked GEMV equal
+    that part's own forward bit for bit, including when the stack is long enough
+    for a workgroup to hold more than two (row, super-block) pairs per thread."""
+    from mold_amd.quantized import Linear, StackedLinear
+    _say(f"stacked modulation GEMV {t.name} m={m}")
+    k = 3072
+    g = torch.Generator(device="cuda").manual_seed(31)
+    parts = []
+    for i, n in enumerate((18432, 18432, 9216, 6144)):
+        w = torch.randn((n, k), device="cuda", generator=g) * 0.02
+        bias = torch.randn((n,), device="cuda", generator=g) * 0.02 if i != 2 else None
+        parts.append((f"part{i}", Linear(QTensor.quantize(dev, w, t), bias)))
+        del w
+    stack = StackedLinear(dev, parts)
+    assert stack.linear.matmul.w.shape == (52224, k)
+    x = torch.randn((m, k), device="cuda", generator=g)
+    ys = stack.forward(x)
+    for name, lin in parts:
+        ref = lin.forward(x)
+        assert torch.equal(ys[name], ref), name
+    # one part anchored to the f64 product (bias-free part)
+    qt = parts[2][1].matmul.w
+    n2 = qt.shape[0]
+    _gemv_check(t, x.cpu().numpy(), ys["part2"].cpu().numpy(), qt.data(), n2, k)
+    with pytest.raises(ValueError):
+        StackedLinear(dev, [parts[0], ("other_k", Linear(QTensor.quantize(
+            dev, torch.zeros((64, 256), device="cuda"), t)))])
+
+
 # ------------------------------------------------------------- quantizer
 
 def _quant_inputs(k, seed):

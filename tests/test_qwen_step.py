@@ -206,10 +206,16 @@ def test_qwen_step_tiny_matches_dequantized_reference():
     err = _rel(o, ref.numpy())
     print(f"[qwen] rel-L2 vs f64 dequantized reference: {err:.3e}", flush=True)
     assert err <= STEP_TOL, err
-    # the serial (single-stream) order gives the same values
+    # the serial (single-stream) order gives the same values, and so do the
+    # modulations run one GEMV per block instead of one stacked GEMV
     ser = Q.QwenImageStep(params, overlap=False).forward(**inp)
+    sep = Q.QwenImageStep(params)
+    sep.stack_modulations = False
+    out_sep = sep.forward(**inp)
     torch.cuda.synchronize()
+    assert step._mod_stack is not None and sep._mod_stack is None
     assert torch.equal(out, ser)
+    assert torch.equal(out, out_sep)
 
 
 @pytest.mark.gpu
@@ -236,8 +242,12 @@ def test_qwen_cfg_batch2_matches_two_single_forwards():
     out_b = step.forward_batched(img2, txt2, t2, inp["grid"], txt_valid=[40, nv])
     c0 = step.forward(inp["img"], inp["txt"], inp["t"], inp["grid"])
     u0 = step.forward(inp["img"], txt_u[:nv].contiguous(), inp["t"], inp["grid"])
+    sep = Q.QwenImageStep(params)
+    sep.stack_modulations = False
+    out_sep = sep.forward_batched(img2, txt2, t2, inp["grid"], txt_valid=[40, nv])
     torch.cuda.synchronize()
     assert torch.equal(out, out_b), "batched forward is not deterministic"
+    assert torch.equal(out, out_sep), "stacked (M = 2) and per-block modulation GEMVs differ"
     assert out.shape == (2,) + tuple(c0.shape) and torch.isfinite(out).all().item()
     e0, e1 = _rel(out[0].cpu().numpy(), c0.cpu().numpy()), _rel(out[1].cpu().numpy(), u0.cpu().numpy())
     print(f"[qwen] batched vs single: cond {e0:.2e}  uncond(masked) {e1:.2e}", flush=True)
