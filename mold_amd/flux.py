@@ -463,10 +463,10 @@ class FluxStep:
 
     def _stacked_mods(self, vec):
         from .quantized import StackedLinear
-        if self._mod_stack is None:
-            lin = self.p.lin[self.modulation_names()[0]]
-            self._mod_stack = StackedLinear(lin.matmul.w.device,
-                                            [(nm, self.p.lin[nm]) for nm in self.modulation_names()])
+        parts = [(nm, self.p.lin[nm]) for nm in self.modulation_names()]
+        if self._mod_stack is None or not self._mod_stack.matches(parts):   # built once, rebuilt if a part changed
+            self._mod_stack = None
+            self._mod_stack = StackedLinear(parts[0][1].matmul.w.device, parts)
         return self._mod_stack.forward(silu(vec))
 
     def _qkv(self, prefix, x, qn, kn):

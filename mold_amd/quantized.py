@@ -305,8 +305,9 @@ class StackedLinear:
     stacked, a step's modulations are one launch streaming every modulation
     weight once.  Each output row is computed by the same per-row arithmetic
     as in the part's own forward, so the outputs are identical.  The stacked
-    weight is a byte copy of the parts' GGUF blocks (same type and k); the
-    parts stay usable on their own."""
+    weight is a byte copy of the parts' GGUF blocks (same type and k), taken
+    when the stack is built; the parts stay usable on their own, and a part
+    replaced afterwards is seen by `matches` (callers rebuild the stack)."""
 
     def __init__(self, device: Device, parts: Sequence[Tuple[str, Linear]]):
         torch = _torch()
@@ -315,6 +316,8 @@ class StackedLinear:
         w0 = parts[0][1].matmul.w
         dtype, k = w0.dtype(), w0.shape[1]
         self.names, self.offsets = [], {}
+        self._ids = [(name, id(lin), id(lin.matmul.w), id(lin.bias)) for name, lin in parts]
+        self._keep = [lin for _, lin in parts]  # the ids above stay unique while the stack lives
         blocks, biases, row = [], [], 0
         for name, lin in parts:
             w = lin.matmul.w
@@ -330,6 +333,10 @@ class StackedLinear:
             row += n
         qt = QTensor.from_blocks(device, dtype, (row, k), np.concatenate(blocks))
         self.linear = Linear(qt, torch.cat([b.reshape(-1).float() for b in biases]).contiguous())
+
+    def matches(self, parts: Sequence[Tuple[str, Linear]]) -> bool:
+        """True when `parts` are the very Linear objects (weights and biases) stacked."""
+        return [(name, id(lin), id(lin.matmul.w), id(lin.bias)) for name, lin in parts] == self._ids
 
     def forward(self, x, out_dtype=None, stream=None) -> Dict[str, object]:
         """{part name: its output [..., n_part]} (column views of one result)."""

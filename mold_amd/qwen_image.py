@@ -256,10 +256,10 @@ class QwenImageStep:
         self._mods = None
         if not (self.stack_modulations and ts.is_cuda and blocks is None):
             return
-        if self._mod_stack is None:
-            names = self.modulation_names()
-            self._mod_stack = StackedLinear(self.p.lin[names[0]].matmul.w.device,
-                                            [(nm, self.p.lin[nm]) for nm in names])
+        parts = [(nm, self.p.lin[nm]) for nm in self.modulation_names()]
+        if self._mod_stack is None or not self._mod_stack.matches(parts):   # built once, rebuilt if a part changed
+            self._mod_stack = None
+            self._mod_stack = StackedLinear(parts[0][1].matmul.w.device, parts)
         self._mods = self._mod_stack.forward(ts)
 
     def _modf(self, name, ts):

@@ -213,3 +213,16 @@ def test_flux_step_tiny_matches_dequantized_reference():
     err = _rel(o, ref.numpy())
     print(f"[flux] rel-L2 vs f64 dequantized reference: {err:.3e}", flush=True)
     assert err <= STEP_TOL, err
+    # a modulation linear replaced after the stack was built is picked up (the
+    # step rebuilds its stack): stacked and per-block forwards still agree
+    nm = step.modulation_names()[0]
+    old = params.lin[nm]
+    g = torch.Generator(device="cuda").manual_seed(99)
+    w2 = torch.randn(old.matmul.w.shape, device="cuda", generator=g) * 0.02
+    params.lin[nm] = mold_amd.Linear(mold_amd.QTensor.quantize(dev, w2, old.matmul.w.dtype()), old.bias)
+    stack_before = step._mod_stack
+    out2, out2_sep = step.forward(**inp), sep.forward(**inp)
+    torch.cuda.synchronize()
+    params.lin[nm] = old
+    assert step._mod_stack is not stack_before
+    assert torch.equal(out2, out2_sep) and not torch.equal(out2, out)
