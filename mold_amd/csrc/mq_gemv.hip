@@ -2,7 +2,10 @@
 // m <= 8 (FLUX/Qwen adaLN modulation, final-layer modulation: m = batch).
 //
 // HBM-bound: every weight byte is read exactly once.  Q4_K weights take
-// gemv_q4k_kernel (below).  The generic kernel (other types): a workgroup
+// gemv_q4k_kernel and the other types gemv_frag_kernel (both below, one
+// workgroup per CU over consecutive rows); where those do not apply (LDS
+// bounds; for the other types also K not a multiple of 256 or m > 4) the
+// generic kernel runs: a workgroup
 // owns one 64-row weight tile and a slice of K; lane r of every wave decodes
 // row r, so each wave load of a 16-byte chunk plane reads one contiguous
 // 1 KiB (see the tiled layout in mq_common.h).  The eight waves split the
