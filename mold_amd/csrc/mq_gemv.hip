@@ -130,10 +130,12 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 // the same number of weight bytes) over all of K.  Thread t takes the
 // (row, super-block) pairs p = t, t + 512, ... (row fastest, so a wave's
 // 16-byte loads of one chunk plane read consecutive rows of the tiled
-// layout), and issues the loads of its first pair before anything else:
-// the weight stream starts at once and the Q8_K staging of x runs while it is
-// in flight: 16-lane group g (of 32) quantizes items g, g + 32, ... (item =
-// one row of x over one super-block) into LDS, 16 elements per lane.
+// layout).  x is loaded first and the weight loads start once the whole
+// workgroup's x has landed (x, read by every workgroup, otherwise queues
+// behind the weight stream in the memory system and the Q8_K staging, on
+// which every dot waits, starts late); the staging then runs while the first
+// pairs stream in: 16-lane group g (of 32) quantizes items g, g + 32, ...
+// (item = one row of x over one super-block) into LDS, 16 elements per lane.
 // Each pair's integer dot reads its 32 Q8_K bytes per 16-byte weight chunk
 // from LDS: 3 + 2M VALU ops per 8 weights.  The pairs' f32 partials go to
 // LDS and thread (row, m) adds them in super-block order (deterministic).
@@ -225,11 +227,9 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   };
 
   // 1. x into LDS by direct loads (item j = sb * M + m is row m's elements
-  //    sb*256 .. +255: one 1 KiB load for f32, half a wave's for bf16), then
-  //    the first pair's weights (index clamped, so every load is
-  //    unconditional).  The explicit wait below leaves the 10 loads issued
-  //    after x's in flight (8 chunk loads, d/dmin and the scale record, none
-  //    of which can merge), so only x has landed.
+  //    sb*256 .. +255: one 1 KiB load for f32, half a wave's for bf16); once
+  //    every wave's x has landed, the first pair's weights (index clamped, so
+  //    every load is unconditional).
   const int nitems = nb * M;
   constexpr int kWaves = kQ4kThreads / 64;
   {
@@ -249,9 +249,9 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     }
   }
   Q4kPair slot[kOne ? 1 : 2];
-  load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
-  asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's x
   __syncthreads();
+  load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
 
   // 2. Q8_K staging: one item per 16-lane group (32 groups, every one at
   //    once); lane L of a group holds elements 16L..16L+15, half of sub-block
