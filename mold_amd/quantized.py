@@ -303,8 +303,10 @@ class StackedLinear:
     `vec`, Qwen-Image's `temb`) through their own adaLN modulation linear
     (flux/offload.rs:143-156 and :282-283, qwen_image/quantized_transformer.rs:869-881);
     stacked, a step's modulations are one launch streaming every modulation
-    weight once.  Each output row is computed by the same per-row arithmetic
-    as in the part's own forward, so the outputs are identical.  The stacked
+    weight once.  At GEMV sizes (m <= 8) each output row is computed by the
+    same per-row arithmetic as in the part's own forward, so the outputs are
+    identical; a larger m runs the GEMM, which may split K differently for the
+    tiles of a partial last round (same values within f32 rounding).  The stacked
     weight is a byte copy of the parts' GGUF blocks (same type and k), taken
     when the stack is built; the parts stay usable on their own, and a part
     replaced afterwards is seen by `matches` (callers rebuild the stack)."""
@@ -317,7 +319,8 @@ class StackedLinear:
         dtype, k = w0.dtype(), w0.shape[1]
         self.names, self.offsets = [], {}
         self._ids = [(name, id(lin), id(lin.matmul.w), id(lin.bias)) for name, lin in parts]
-        self._keep = [lin for _, lin in parts]  # the ids above stay unique while the stack lives
+        # the objects behind the ids stay alive (so no id is reused) while the stack lives
+        self._keep = [(lin, lin.matmul.w, lin.bias) for _, lin in parts]
         blocks, biases, row = [], [], 0
         for name, lin in parts:
             w = lin.matmul.w
