@@ -69,6 +69,17 @@ template <>
 __device__ __forceinline__ void store_out<float>(float *p, float v) { *p = v; }
 template <>
 __device__ __forceinline__ void store_out<__bf16>(__bf16 *p, float v) { *p = (__bf16)v; }
+// Output stores of whole tiles: y is never read back by the kernel, so f32
+// outputs are stored nontemporal (they do not displace the activation panels
+// and weight tiles other workgroups re-read from L2: headline 4608x3072->21504
+// f32 ~0.7 % faster, same values).
+template <typename OUT>
+__device__ __forceinline__ void store_out_stream(OUT *p, float v) {
+  if constexpr (std::is_same_v<OUT, float>)
+    __builtin_nontemporal_store(v, p);
+  else
+    store_out<OUT>(p, v);
+}
 
 // y = v, or with a gate (f32 output only) the gated residual update
 // y = r + g * v of the DiT blocks, r read through its own pointer `res`
@@ -434,13 +445,14 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
 #pragma unroll
         for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
+          for (int e = 0; e < 16; ++e)
+            store_out_stream<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
       } else {
 #pragma unroll
         for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
-            store_out<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, act_out<OUT>(acc[mb][e] + bv, MQ_ACT_GELU_));
+            store_out_stream<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, act_out<OUT>(acc[mb][e] + bv, MQ_ACT_GELU_));
       }
       return;
     }
