@@ -83,6 +83,16 @@ int mq_ctx_reserve_scratch(mq_ctx *ctx, size_t bytes);
  * have to grow the workspace of a stream under capture fails with
  * MQ_E_INVALID instead.  Optional. */
 int mq_ctx_reserve_stream_scratch(mq_ctx *ctx, void *stream, size_t bytes);
+/* Whether GEMMs on `stream` may split K when their last round of tiles over
+ * the CUs is partial (default: enabled, for every stream).  The split fills
+ * the CUs a lone GEMM's partial round leaves idle, at the cost of f32 partial
+ * sums and a reduce launch; on a stream whose GEMMs run beside another
+ * stream's (mold's DiT blocks: the text-token linears beside the image-token
+ * ones), those CUs are not idle and the split only adds traffic, so such a
+ * stream turns it off.  No counterpart in candle, whose device runs one
+ * stream; its callers are multi-stream callers such as the DiT block
+ * drivers. */
+int mq_ctx_set_stream_tail_split(mq_ctx *ctx, void *stream, int enabled);
 /* Workspace bytes a quantized matmul of `m` rows against w needs (gated != 0
  * for mq_qmatmul_gated_add), the maximum over every x placement and stride:
  * the size to reserve before capturing such calls into a graph.  No

@@ -26,6 +26,7 @@ SIGNATURES = {
     "mq_ctx_reserve_arena": (_int, [_vp, _sz]),
     "mq_ctx_reserve_scratch": (_int, [_vp, _sz]),
     "mq_ctx_reserve_stream_scratch": (_int, [_vp, _vp, _sz]),
+    "mq_ctx_set_stream_tail_split": (_int, [_vp, _vp, _int]),
     "mq_qmatmul_workspace_size": (_int, [_vp, _vp, _int, _i64, _int, ctypes.POINTER(_sz)]),
     "mq_qtensor_upload": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _pp]),
     "mq_qtensor_from_device": (_int, [_vp, _int, _i64, _i64, _vp, _sz, _vp, _pp]),

@@ -39,6 +39,9 @@ struct mq_ctx {
   };
   std::vector<Ws> ws;
   std::vector<void *> retired;
+  // Streams whose GEMMs never split K over a partial last round of tiles
+  // (mq_ctx_set_stream_tail_split).
+  std::vector<hipStream_t> no_tail_split;
   size_t ws_floor = 0;  // mq_ctx_reserve_scratch: minimum size of every workspace
   // Upload staging: a device buffer for raw GGUF blocks (grows, kept) and two
   // pinned host buffers for file reads (allocated on the first GGUF load).
@@ -184,7 +187,7 @@ struct Plan {
 };
 
 Plan plan_qmatmul(const mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
-                  bool gated) {
+                  bool gated, bool tail_split = true) {
   Plan p;
   const int64_t n = w->n, k = w->k;
   if (m <= kGemvMaxM && !gated) {
@@ -199,13 +202,17 @@ Plan plan_qmatmul(const mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_d
         !(x_dtype == MQ_BF16 && k == p.kp && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0);
     const int64_t lda = p.stage_gemm ? p.kp : ldx;
     p.stage_bytes = p.stage_gemm ? (size_t)m * p.kp * sizeof(__bf16) : 0;
-    p.tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
+    if (tail_split) p.tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
     if (p.tail.kparts > 1 && gemm_fast_ok(w->dtype, m, k, lda)) p.part_bytes = gemm_tail_bytes(p.tail, m, n);
     else p.tail.kparts = 1;
   }
   p.part_off = align256(p.stage_bytes);
   p.total = p.part_bytes ? p.part_off + p.part_bytes : p.stage_bytes;
   return p;
+}
+
+bool tail_split_on(const mq_ctx *ctx, hipStream_t s) {
+  return std::find(ctx->no_tail_split.begin(), ctx->no_tail_split.end(), s) == ctx->no_tail_split.end();
 }
 
 // Runs one planned call with its scratch at `ws` (p.total bytes).
@@ -419,6 +426,16 @@ int mq_ctx_reserve_stream_scratch(mq_ctx *ctx, void *stream, size_t bytes) {
   return stream_workspace(ctx, static_cast<hipStream_t>(stream), bytes, &p);
 }
 
+int mq_ctx_set_stream_tail_split(mq_ctx *ctx, void *stream, int enabled) {
+  if (!ctx) return fail(MQ_E_INVALID, "ctx is NULL");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  auto &v = ctx->no_tail_split;
+  const auto it = std::find(v.begin(), v.end(), s);
+  if (enabled && it != v.end()) v.erase(it);
+  if (!enabled && it == v.end()) v.push_back(s);
+  return MQ_OK;
+}
+
 int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *dev_blocks, size_t nbytes,
                            void *stream, mq_qtensor **out) {
   if (!ctx || !out || !dev_blocks) return fail(MQ_E_INVALID, "mq_qtensor_from_device: NULL argument");
@@ -555,7 +572,7 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
   if (rc || m == 0) return rc;
   DeviceGuard g(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false);
+  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false, tail_split_on(ctx, s));
   uint8_t *ws = nullptr;
   if (p.total) {
     rc = stream_workspace(ctx, s, p.total, &ws);
@@ -569,7 +586,8 @@ int mq_qmatmul_noalloc(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dt
   int rc = check_qmatmul_args("mq_qmatmul_noalloc", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
   if (rc || m == 0) return rc;
   DeviceGuard g(ctx->device);
-  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false);
+  const Plan p =
+      plan_qmatmul(ctx, w, x, x_dtype, m, ldx, false, tail_split_on(ctx, static_cast<hipStream_t>(stream)));
   if (p.total > MQ_NOALLOC_SCRATCH_BYTES)
     return fail(MQ_E_INVALID,
                 "mq_qmatmul_noalloc: this call needs %zu bytes of scratch, more than its fixed %zu bytes "
@@ -590,7 +608,7 @@ int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_
   DeviceGuard g(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
   // every m takes the GEMM kernel: its epilogue holds the gated update
-  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, true);
+  const Plan p = plan_qmatmul(ctx, w, x, x_dtype, m, ldx, true, tail_split_on(ctx, s));
   uint8_t *ws = nullptr;
   if (p.total) {
     rc = stream_workspace(ctx, s, p.total, &ws);

@@ -229,6 +229,21 @@ def aux_stream(device):
     return s
 
 
+def text_stream(device, ctx):
+    """aux_stream(device) for a block's text-token linears, with libmoldq's
+    tail K split turned off on it for the library context `ctx` (a
+    mold_amd.Device): those GEMMs run beside the image stream's, which keep
+    the CUs busy, so splitting their partial last round of tiles only adds
+    partial-sum traffic and reduce launches (FLUX step 0.7-0.9 % and
+    Qwen-Image 1.5-3.7 % faster, same-box pairs on two boxes)."""
+    s = aux_stream(device)
+    done = ctx.__dict__.setdefault("_tail_split_off", set())
+    if s.cuda_stream not in done:
+        ctx.set_stream_tail_split(s, False)
+        done.add(s.cuda_stream)
+    return s
+
+
 ATTENTION_BACKEND = {"name": None}
 
 
@@ -559,7 +574,7 @@ class FluxStep:
         total = lt + img.shape[0]
         q, k, v = new_heads(H, self._joint_len(total), img.device, valid=total)
         main = torch.cuda.current_stream(img.device)
-        aux = aux_stream(img.device)
+        aux = text_stream(img.device, self.p.lin[p + "txt_attn.qkv"].matmul.w.device)
         aux.wait_stream(main)
         with torch.cuda.stream(aux):
             ty = self.p.lin[p + "txt_attn.qkv"].forward(self._modulate(txt, tm[0], tm[1]), out_dtype=bf16)

@@ -92,6 +92,12 @@ class Device:
         """Grow one stream's workspace now (e.g. before capturing it in a graph)."""
         check(_lib.load().mq_ctx_reserve_stream_scratch(self._h, _stream_ptr(stream), nbytes))
 
+    def set_stream_tail_split(self, stream, enabled: bool) -> None:
+        """mq_ctx_set_stream_tail_split: whether GEMMs on `stream` may split K
+        over a partial last round of tiles (off for a stream whose GEMMs run
+        beside another stream's)."""
+        check(_lib.load().mq_ctx_set_stream_tail_split(self._h, _stream_ptr(stream), int(bool(enabled))))
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             _lib.load().mq_ctx_destroy(self._h)

@@ -60,7 +60,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
-from .flux import apply_rope, attention_bf16, attention_bf16_batch, aux_stream, gelu_tanh, layer_norm, padded_len, run_guarded, silu
+from .flux import apply_rope, attention_bf16, attention_bf16_batch, gelu_tanh, layer_norm, padded_len, run_guarded, silu, text_stream
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
 MAX_PERIOD = 10000.0
@@ -394,7 +394,7 @@ class QwenImageStep:
         use = self.overlap if self.overlap is not None else x.is_cuda
         if not use or not x.is_cuda or self.gemm_dtype != torch.bfloat16:
             return None
-        return aux_stream(x.device)
+        return text_stream(x.device, self.p.lin["txt_in"].matmul.w.device)
 
     def stems(self, img, txt, t):
         import torch

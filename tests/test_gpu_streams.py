@@ -9,6 +9,8 @@
   the eager call, with eager work and synchronizations between replays; a call
   that would have to grow a capturing stream's workspace is refused with a
   clear error instead of allocating.
+* A stream with the tail K split turned off runs a partial-round GEMM unsplit
+  (same values up to the K summation order) and split again once turned on.
 * A GGUF file is loaded through the pinned, double-buffered upload (tensors
   larger than one 16 MiB chunk) and reads back byte-identical.
 """
@@ -69,6 +71,36 @@ def test_two_streams_f32_input_gemms(torch):
     blocks = wa.w.data()
     ref = O.matmul_f64(int(GgmlDType.Q4_K), xa[torch.from_numpy(rows).cuda()].cpu().numpy(), blocks, 3072, 3072)
     assert O.rel_l2(ref_a[torch.from_numpy(rows).cuda()].cpu().numpy(), ref) <= 1e-2
+
+
+def test_stream_without_tail_split(torch):
+    """mq_ctx_set_stream_tail_split: a GEMM whose last round of tiles is partial
+    (m=512: 2 x 24 tiles, split 8 ways by default) runs unsplit on a stream with
+    the split turned off, with the same values up to the order of the K sum, and
+    split again once it is turned back on (bit-identical to the default)."""
+    dev = mold_amd.Device(0)
+    _say("tail split off on one stream: Q4_K m=512 k=3072 n=3072, bf16 x")
+    w = QMatMul(_qt(dev, "Q4_K", 3072, 3072, 4))
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn((512, 3072), device="cuda", generator=g).to(torch.bfloat16)
+    ref = w.forward(x, out_dtype=torch.float32)          # current stream: split
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    dev.set_stream_tail_split(s, False)
+    with torch.cuda.stream(s):
+        y_off = w.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    dev.set_stream_tail_split(s, True)
+    with torch.cuda.stream(s):
+        y_on = w.forward(x, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(y_on.view(torch.int32), ref.view(torch.int32))
+    assert not torch.equal(y_off.view(torch.int32), ref.view(torch.int32)), "the split setting had no effect"
+    assert torch.allclose(y_off, ref, rtol=1e-5, atol=1e-5)
+    rows = np.array([0, 255, 511])
+    ri = torch.from_numpy(rows).cuda()
+    exact = O.matmul_f64(int(GgmlDType.Q4_K), x[ri].float().cpu().numpy(), w.w.data(), 3072, 3072)
+    assert O.rel_l2(y_off[ri].cpu().numpy(), exact) <= 1e-2
 
 
 def test_workspace_growth_keeps_queued_work(torch):
