@@ -127,7 +127,9 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
 //
 // HBM-bound layout of the work: one 512-thread workgroup per CU owns `rows`
 // consecutive output rows (ceil(n / CUs): 72 at n = 18432, so every CU reads
-// the same number of weight bytes) over all of K.  Thread t takes the
+// the same number of weight bytes) over all of K; where the LDS would not hold
+// that many rows' partials (the steps' stacked modulation launches, ~1M rows)
+// workgroups take fewer rows and several run on each CU in turn.  Thread t takes the
 // (row, super-block) pairs p = t, t + 512, ... (row fastest, so a wave's
 // 16-byte loads of one chunk plane read consecutive rows of the tiled
 // layout).  x is loaded first and the weight loads start once the whole
