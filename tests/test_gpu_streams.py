@@ -101,6 +101,19 @@ def test_stream_without_tail_split(torch):
     ri = torch.from_numpy(rows).cuda()
     exact = O.matmul_f64(int(GgmlDType.Q4_K), x[ri].float().cpu().numpy(), w.w.data(), 3072, 3072)
     assert O.rel_l2(y_off[ri].cpu().numpy(), exact) <= 1e-2
+    # the gated residual update (the blocks' out-projections) on the unsplit stream
+    lin = mold_amd.Linear(w.w, torch.randn(3072, device="cuda", generator=g) * 0.02)
+    gate = torch.randn(3072, device="cuda", generator=g)
+    res0 = torch.randn((512, 3072), device="cuda", generator=g)
+    r_split, r_off = res0.clone(), res0.clone()
+    lin.gated_add(x, gate, r_split)
+    torch.cuda.synchronize()
+    dev.set_stream_tail_split(s, False)
+    with torch.cuda.stream(s):
+        lin.gated_add(x, gate, r_off)
+    torch.cuda.synchronize()
+    assert torch.allclose(r_off, r_split, rtol=1e-5, atol=1e-5)
+    assert torch.allclose(r_off - res0, gate * (ref + lin.bias), rtol=1e-3, atol=1e-4)
 
 
 def test_workspace_growth_keeps_queued_work(torch):
