@@ -137,8 +137,8 @@ class QTensor:
         self._gguf_bytes = gb.value
         self.device_bytes = db.value
 
-    # candle: QTensor::quantize is CPU-side fixture generation here (oracle);
-    # loading GGUF blocks is the upload path below.
+    # candle: a QTensor from GGUF blocks already in host memory (the upload
+    # path); QTensor::quantize_onto is `quantize` below, on the GPU.
     @classmethod
     def from_blocks(cls, device: Device, dtype: GgmlDType, shape: Sequence[int], blocks) -> "QTensor":
         """Upload GGUF blocks from host memory (bytes / numpy uint8)."""
