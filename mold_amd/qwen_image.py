@@ -454,10 +454,12 @@ class QwenImageStep:
         return out
 
     def _gated_rows(self, name, h, mods, j, res, B):
-        """res[b rows] += gate_b * lin(h[b rows]) per element (GEMM epilogue)."""
+        """res[b rows] += gate_b * lin(h_b) per element (GEMM epilogue), h_b
+        element b's rows of h, or h[b] when h is a list of per-element inputs."""
         lx = res.shape[0] // B
         for b in range(B):
-            self.p.lin[name].gated_add(h[b * lx:(b + 1) * lx], mods[b][j], res[b * lx:(b + 1) * lx])
+            hb = h[b] if isinstance(h, (list, tuple)) else h[b * lx:(b + 1) * lx]
+            self.p.lin[name].gated_add(hb, mods[b][j], res[b * lx:(b + 1) * lx])
         return res
 
     def block_batched(self, i, img, txt, ts, rope, B, valid):
@@ -477,8 +479,6 @@ class QwenImageStep:
         hq, hk, hv = new_heads(H, padded_len(total) if self.pad_attention else total, img.device, valid=total,
                                batch=B)
         heads_b = [(hq[b], hk[b], hv[b]) for b in range(B)]
-        i_att = torch.empty((B * L, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
-        t_att = torch.empty((B * lt, H * cfg.attention_head_dim), dtype=torch.bfloat16, device=img.device)
         # text stream on `aux` as in block(): its modulate, qkv projection and
         # q/k norm overlap the image qkv projection, its tail overlaps the image
         # out-projection and MLP; tensors shared across the streams are recorded
@@ -513,9 +513,10 @@ class QwenImageStep:
         else:   # the guarded rerun: exact attention over the kept keys
             from .flux import _attention_chunked
             a = [_attention_chunked(*(t[:, :total] for t in heads_b[b]), drops[b]) for b in range(B)]
-        for b in range(B):
-            t_att[b * lt:(b + 1) * lt] = a[b][:lt]
-            i_att[b * L:(b + 1) * L] = a[b][lt:]
+        # each element's text and image rows of the attention output feed its
+        # out-projections in place (strided rows, no copy)
+        t_att = [a[b][:lt] for b in range(B)]
+        i_att = [a[b][lt:] for b in range(B)]
         if aux is not None:
             aux.wait_stream(main)
         with on_aux():
@@ -524,7 +525,8 @@ class QwenImageStep:
                                                          out_dtype=torch.bfloat16)
             txt = self._gated_rows(p + "txt_mlp.net.2", ht, tm, 5, txt, B)
         if aux is not None:
-            t_att.record_stream(aux)
+            for t in (a if isinstance(a, list) else [a]):
+                t.record_stream(aux)
         img = self._gated_rows(p + "attn.to_out.0", i_att, im, 2, img, B)
         h = P.lin[p + "img_mlp.net.0.proj"].forward(self._mod_rows(img, im, 3, 4, B), act=ACT_GELU_TANH,
                                                     out_dtype=torch.bfloat16)
