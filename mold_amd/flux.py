@@ -295,7 +295,8 @@ def _no_fused_kernel(err: RuntimeError) -> bool:
                                   "invalid device function", "not compiled"))
 
 
-def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optional[Tuple[int, int]] = None):
+def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optional[Tuple[int, int]] = None,
+                   out=None):
     """softmax(q k^T / sqrt(d)) v for q, k, v [H, L, D] -> [valid, H*D] bf16.
 
     Runs PyTorch's fused attention in bf16 (f32 softmax accumulation inside; on
@@ -318,6 +319,11 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
     padded tail of a shorter prompt in a CFG batch): their k and v rows must be
     zero, so they are removed by the same correction (n_pad counts them too).
 
+    `out`, a bf16 [valid, H*D] tensor whose rows may be strided (a column block
+    of a wider buffer), receives the result in place of a new tensor: the
+    correction pass writes it there, the unpadded path copies its [H, L, D]
+    output there once.
+
     Where no fused kernel serves the device, it falls back to the exact
     head-chunked path on the valid rows (any other error propagates).  The
     backend used is recorded in ATTENTION_BACKEND."""
@@ -327,15 +333,18 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
     valid = l if valid is None else valid
     qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
     n_drop = 0 if drop is None else max(0, drop[1] - drop[0])
+    if out is not None and (out.shape != (valid, h * d) or out.dtype != torch.bfloat16 or out.stride(1) != 1):
+        raise ValueError(f"attention_bf16: out must be bf16 [{valid}, {h * d}] with unit column stride")
     if ATTENTION_BACKEND["name"] in (None, "fused"):
         try:
             if valid < l or n_drop:
-                out, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
-                                                                                  True)[:2]
+                o_pad, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None],
+                                                                                    None, True)[:2]
                 pad_share = (l - valid + n_drop) * torch.exp(-lse[0, :, :valid])  # [h, valid] f32, 1 - s
                 # one pass: correct in f32, round to bf16, write the [valid, h, d] layout
-                res = torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device)
-                torch.mul(out[0, :, :valid].transpose(0, 1), (1.0 / (1.0 - pad_share)).transpose(0, 1)[..., None],
+                res = (out.view(valid, h, d) if out is not None
+                       else torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device))
+                torch.mul(o_pad[0, :, :valid].transpose(0, 1), (1.0 / (1.0 - pad_share)).transpose(0, 1)[..., None],
                           out=res)
                 if guard is not None:
                     torch.maximum(guard, pad_share.amax(), out=guard)
@@ -346,17 +355,24 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
                         exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid], drop)
                         res[:, heads] = exact.view(valid, heads.numel(), d)
                 ATTENTION_BACKEND["name"] = "fused"
-                return res.reshape(valid, h * d)
+                return out if out is not None else res.reshape(valid, h * d)
             else:
                 with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
                     o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
             ATTENTION_BACKEND["name"] = "fused"
+            if out is not None:
+                out.view(valid, h, d).copy_(o.transpose(0, 1))
+                return out
             return o.transpose(0, 1).reshape(valid, h * d)
         except RuntimeError as err:
             if not _no_fused_kernel(err):
                 raise
             ATTENTION_BACKEND["name"] = "chunked"
-    return _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid], drop)
+    res = _attention_chunked(qb[:, :valid], kb[:, :valid], vb[:, :valid], drop)
+    if out is not None:
+        out.copy_(res)
+        return out
+    return res
 
 
 _NPAD_CACHE: dict = {}
@@ -507,11 +523,16 @@ class FluxStep:
             return self.p.lin[name].gated_add(h, gate, res)
         return res + gate * self.p.lin[name].forward(h, out_dtype=torch.float32)
 
-    def _attn_padded(self, q, k, v, valid):
-        """Attention over the fused path's padded joint buffers (rows >= valid zero)."""
+    def _attn_padded(self, q, k, v, valid, out=None):
+        """Attention over the fused path's padded joint buffers (rows >= valid zero),
+        written into `out` ([valid, H*D], rows may be strided) when given."""
         if self.attn is attention_bf16:
-            return attention_bf16(q, k, v, valid, guard=self._guard)
-        return self.attn(q[:, :valid], k[:, :valid], v[:, :valid])
+            return attention_bf16(q, k, v, valid, guard=self._guard, out=out)
+        a = self.attn(q[:, :valid], k[:, :valid], v[:, :valid])
+        if out is not None:
+            out.copy_(a)
+            return out
+        return a
 
     def _joint_len(self, total: int) -> int:
         """Rows of the joint attention buffers: padded to a multiple of 256 unless
@@ -611,21 +632,19 @@ class FluxStep:
         y_dtype = torch.bfloat16 if self._fused(x) and self.bf16_projections else torch.float32
         y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=y_dtype)
         L, h = x.shape[0], cfg.hidden_size
+        cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
         if self._fused(x):
-            a = self._attn_padded(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")],
-                                                     cos, sin), L)
+            # attention writes its rows straight into linear2's concatenated input
+            self._attn_padded(*self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")],
+                                                 cos, sin), L, out=cat[:, :h])
+            from .fused import gelu_tanh_bf16
+            gelu_tanh_bf16(y[:, 3 * h:], cat[:, h:])
         else:
             qkv = y[:, :3 * h].reshape(L, 3, cfg.num_heads, cfg.head_dim)
             q = rms_norm(qkv[:, 0].transpose(0, 1), self.p.dense[p + "norm.query_norm.scale"])
             k = rms_norm(qkv[:, 1].transpose(0, 1), self.p.dense[p + "norm.key_norm.scale"])
             v = qkv[:, 2].transpose(0, 1)
-            a = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
-        cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
-        cat[:, :h] = a
-        if self._fused(x):
-            from .fused import gelu_tanh_bf16
-            gelu_tanh_bf16(y[:, 3 * h:], cat[:, h:])
-        else:
+            cat[:, :h] = self.attn(apply_rope(q, cos, sin), apply_rope(k, cos, sin), v)
             cat[:, h:] = gelu_tanh(y[:, 3 * h:])
         return self._gated(p + "linear2", cat, gate, x)
 

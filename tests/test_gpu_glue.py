@@ -126,6 +126,21 @@ def test_padded_attention_matches_reference(valid, padded):
     assert out.shape == (valid, H * D)
     err = ((out.float() - ref).norm() / ref.norm()).item()
     assert err < 5e-3, err
+    _check_out_block(attention_bf16, (q, k, v, valid), out)
+
+
+def _check_out_block(attn, args, expect):
+    """attn(*args, out=block) with block a strided column block of a wider bf16 buffer
+    (how the single block writes attention into linear2's input): bit-identical to the
+    returned tensor, the buffer's other columns untouched."""
+    valid, hd = expect.shape
+    buf = torch.full((valid, hd + 96), 7.0, dtype=torch.bfloat16, device="cuda")
+    block = buf[:, 32:32 + hd]
+    r = attn(*args, out=block)
+    torch.cuda.synchronize()
+    assert r.data_ptr() == block.data_ptr()
+    assert torch.equal(block, expect)
+    assert bool((buf[:, :32] == 7.0).all()) and bool((buf[:, 32 + hd:] == 7.0).all())
 
 
 def test_batched_padded_attention_with_dropped_keys():
@@ -193,6 +208,7 @@ def test_padded_attention_ill_conditioned_rows_recomputed():
     out = attention_bf16(q, k, v, valid)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all().item()
+    _check_out_block(attention_bf16, (q, k, v, valid), out)
     H, D = q.shape[0], q.shape[2]
     for h in range(H):
         o, r = out.view(valid, H, D)[:, h].double().cpu(), ref.view(valid, H, D)[:, h]
