@@ -242,11 +242,13 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
         dma16(x + m * ldx + sb * 256 + 4 * lane, lbase + j * 1024);
       }
     } else {
-      // two items per load: lanes 0-31 item j, lanes 32-63 item j + 1
+      // two items per load: lanes 0-31 item j, lanes 32-63 item j + 1; for an
+      // odd item count the last load issues lanes 0-31 only (lane i writes LDS
+      // byte 16 i on, so lanes 32-63 would write past the x region, and past
+      // the allocation when few rows' partials follow it)
       for (int j = 2 * wave; j < nitems; j += 2 * kWaves) {
-        const int jj = j + (lane >> 5) < nitems ? j + (lane >> 5) : j;
-        const int sb = jj / M, m = jj - sb * M;
-        dma16(x + m * ldx + sb * 256 + 8 * (lane & 31), lbase + j * 512);
+        const int sb = (j + (lane >> 5)) / M, m = (j + (lane >> 5)) - sb * M;
+        if (lane < 32 || j + 1 < nitems) dma16(x + m * ldx + sb * 256 + 8 * (lane & 31), lbase + j * 512);
       }
     }
   }

@@ -81,6 +81,7 @@ int gfail(int code, const char *fmt, ...) {
 
 struct Reader {
   FILE *f;
+  uint64_t fsize;  // bytes in the file: no length read from it may exceed what is left
   bool ok = true;
   template <typename T>
   T get() {
@@ -88,9 +89,14 @@ struct Reader {
     if (fread(&v, sizeof(T), 1, f) != 1) ok = false;
     return v;
   }
+  // Bytes between the read position and the end of the file.
+  uint64_t left() const {
+    const off_t pos = ftello(f);
+    return pos < 0 || (uint64_t)pos > fsize ? 0 : fsize - (uint64_t)pos;
+  }
   std::string str() {
     const uint64_t n = get<uint64_t>();
-    if (!ok || n > (1ull << 30)) {
+    if (!ok || n > (1ull << 30) || n > left()) {
       ok = false;
       return {};
     }
@@ -114,19 +120,20 @@ size_t scalar_size(uint32_t t) {
   }
 }
 
-// Skips one array value of element type `et` (nested arrays).
-bool skip_array(Reader &r) {
+// Skips one array value (nested arrays), at most 8 levels deep.
+bool skip_array(Reader &r, int depth) {
   const uint32_t et = r.get<uint32_t>();
   const uint64_t cnt = r.get<uint64_t>();
   if (!r.ok) return false;
   if (et == STR) {
     for (uint64_t i = 0; i < cnt && r.ok; ++i) (void)r.str();
   } else if (et == ARR) {
+    if (depth > 8) return false;  // deeper nesting than any GGUF writer produces
     for (uint64_t i = 0; i < cnt && r.ok; ++i)
-      if (!skip_array(r)) return false;
+      if (!skip_array(r, depth + 1)) return false;
   } else {
     const size_t es = scalar_size(et);
-    if (!es || cnt > (1ull << 34) / es) return false;
+    if (!es || cnt > (1ull << 34) / es || es * cnt > r.left()) return false;
     if (fseeko(r.f, (off_t)(es * cnt), SEEK_CUR) != 0) return false;
   }
   return r.ok;
@@ -143,7 +150,9 @@ bool read_value(Reader &r, Kv &kv) {
     kv.count = r.get<uint64_t>();
     if (!r.ok) return false;
     if (kv.elem_type == STR) {
-      if (kv.count > (1ull << 26)) return false;
+      // every string holds at least its 8-byte length: a count the rest of
+      // the file cannot hold is malformed, and nothing is reserved for it
+      if (kv.count > (1ull << 26) || kv.count > r.left() / 8) return false;
       kv.strs.reserve(kv.count);
       for (uint64_t i = 0; i < kv.count && r.ok; ++i) kv.strs.push_back(r.str());
       return r.ok;
@@ -151,11 +160,11 @@ bool read_value(Reader &r, Kv &kv) {
     if (kv.elem_type == ARR) {
       kv.nested = true;
       for (uint64_t i = 0; i < kv.count && r.ok; ++i)
-        if (!skip_array(r)) return false;
+        if (!skip_array(r, 1)) return false;
       return r.ok;
     }
     const size_t es = scalar_size(kv.elem_type);
-    if (!es || kv.count > (1ull << 30) / es) return false;
+    if (!es || kv.count > (1ull << 30) / es || es * kv.count > r.left()) return false;
     kv.raw.resize(es * kv.count);
     return r.bytes(kv.raw.data(), kv.raw.size());
   }
@@ -189,16 +198,26 @@ int64_t int_at(const Kv &kv, uint64_t e) {
   }
 }
 
-}  // namespace
+// Runs fn(), turning any C++ exception into a status code: nothing is thrown
+// across the C ABI (an allocation the host cannot satisfy is MQ_E_OOM).
+template <typename Fn>
+int no_throw(const char *what, Fn &&fn) {
+  try {
+    return fn();
+  } catch (const std::bad_alloc &) {
+    return gfail(MQ_E_OOM, "%s: out of host memory", what);
+  } catch (...) {
+    return gfail(MQ_E_IO, "%s: unexpected failure", what);
+  }
+}
 
-extern "C" {
-
-int mq_gguf_open(const char *path, mq_gguf **out) {
-  if (!path || !out) return gfail(MQ_E_INVALID, "mq_gguf_open: NULL argument");
-  *out = nullptr;
+int gguf_open(const char *path, mq_gguf **out) {
   std::unique_ptr<FILE, int (*)(FILE *)> file(fopen(path, "rb"), fclose);
   if (!file) return gfail(MQ_E_IO, "cannot open %s", path);
-  Reader r{file.get()};
+  if (fseeko(file.get(), 0, SEEK_END) != 0) return gfail(MQ_E_IO, "cannot seek %s", path);
+  const off_t fend = ftello(file.get());
+  if (fend < 0 || fseeko(file.get(), 0, SEEK_SET) != 0) return gfail(MQ_E_IO, "cannot seek %s", path);
+  Reader r{file.get(), (uint64_t)fend};
   std::unique_ptr<mq_gguf> g(new (std::nothrow) mq_gguf());
   if (!g) return gfail(MQ_E_OOM, "out of host memory");
   g->path = path;
@@ -262,8 +281,7 @@ int mq_gguf_open(const char *path, mq_gguf **out) {
   if (!r.ok) return gfail(MQ_E_IO, "%s: truncated or malformed GGUF header", path);
   const off_t pos = ftello(file.get());
   const uint64_t data_start = ((uint64_t)pos + g->alignment - 1) / g->alignment * g->alignment;
-  fseeko(file.get(), 0, SEEK_END);
-  const uint64_t fsize = (uint64_t)ftello(file.get());
+  const uint64_t fsize = r.fsize;
   for (auto &t : g->tensors) {
     if (t.offset > fsize || t.offset % g->alignment != 0)
       return gfail(MQ_E_IO, "tensor %s: bad data offset %llu", t.name.c_str(), (unsigned long long)t.offset);
@@ -272,6 +290,16 @@ int mq_gguf_open(const char *path, mq_gguf **out) {
   }
   *out = g.release();
   return MQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mq_gguf_open(const char *path, mq_gguf **out) {
+  if (!path || !out) return gfail(MQ_E_INVALID, "mq_gguf_open: NULL argument");
+  *out = nullptr;
+  return no_throw("mq_gguf_open", [&] { return gguf_open(path, out); });
 }
 
 void mq_gguf_close(mq_gguf *g) { delete g; }
@@ -455,16 +483,18 @@ int add_kv(mq_gguf_writer *w, const char *key, uint32_t type, uint32_t elem_type
   if (w->finished) return gfail(MQ_E_INVALID, "GGUF writer: already finished");
   for (const Kv &kv : w->kvs)
     if (kv.key == key) return gfail(MQ_E_INVALID, "GGUF writer: duplicate metadata key %s", key);
-  Kv kv;
-  kv.key = key;
-  kv.type = type;
-  kv.elem_type = elem_type;
-  kv.count = count;
-  if (raw_bytes) kv.raw.assign(static_cast<const uint8_t *>(raw), static_cast<const uint8_t *>(raw) + raw_bytes);
-  if (strs)
-    for (uint64_t i = 0; i < count; ++i) kv.strs.emplace_back(strs[i] ? strs[i] : "");
-  w->kvs.push_back(std::move(kv));
-  return MQ_OK;
+  return no_throw("GGUF writer metadata", [&] {
+    Kv kv;
+    kv.key = key;
+    kv.type = type;
+    kv.elem_type = elem_type;
+    kv.count = count;
+    if (raw_bytes) kv.raw.assign(static_cast<const uint8_t *>(raw), static_cast<const uint8_t *>(raw) + raw_bytes);
+    if (strs)
+      for (uint64_t i = 0; i < count; ++i) kv.strs.emplace_back(strs[i] ? strs[i] : "");
+    w->kvs.push_back(std::move(kv));
+    return (int)MQ_OK;
+  });
 }
 
 int check_tensor_name(const mq_gguf_writer *w, const char *name) {
@@ -487,6 +517,8 @@ size_t tensor_bytes(int dtype, int n_dims, const int64_t *dims) {
   return (size_t)(elems / bs) * ts;
 }
 
+int writer_finish(mq_gguf_writer *w);
+
 }  // namespace
 
 extern "C" {
@@ -497,16 +529,18 @@ int mq_gguf_writer_create(const char *path, uint32_t alignment, mq_gguf_writer *
   if (alignment == 0) alignment = 32;
   if ((alignment & (alignment - 1)) != 0 || alignment > 65536)
     return gfail(MQ_E_INVALID, "GGUF alignment %u is not a power of two", alignment);
-  mq_gguf_writer *w = new (std::nothrow) mq_gguf_writer();
-  if (!w) return gfail(MQ_E_OOM, "out of host memory");
-  w->path = path;
-  w->alignment = alignment;
-  if (alignment != 32) {
-    const uint32_t a = alignment;
-    add_kv(w, "general.alignment", U32, U32, 1, &a, 4, nullptr);
-  }
-  *out = w;
-  return MQ_OK;
+  return no_throw("mq_gguf_writer_create", [&] {
+    std::unique_ptr<mq_gguf_writer> w(new mq_gguf_writer());
+    w->path = path;
+    w->alignment = alignment;
+    if (alignment != 32) {
+      const uint32_t a = alignment;
+      const int rc = add_kv(w.get(), "general.alignment", U32, U32, 1, &a, 4, nullptr);
+      if (rc) return rc;
+    }
+    *out = w.release();
+    return (int)MQ_OK;
+  });
 }
 
 void mq_gguf_writer_free(mq_gguf_writer *w) { delete w; }
@@ -544,18 +578,16 @@ int mq_gguf_writer_add_tensor(mq_gguf_writer *w, const char *name, int dtype, in
   if (!want) return gfail(MQ_E_INVALID, "GGUF writer: tensor %s has bad type %d or dims", name, dtype);
   if (want != nbytes) return gfail(MQ_E_INVALID, "GGUF writer: tensor %s needs %zu bytes, got %zu", name, want, nbytes);
   WTensor t;
-  t.name = name;
   t.dtype = dtype;
   t.n_dims = n_dims;
   for (int d = 0; d < n_dims; ++d) t.dims[d] = (uint64_t)dims[d];
   t.nbytes = nbytes;
-  try {
+  return no_throw("GGUF writer tensor", [&] {
+    t.name = name;
     t.data.assign(static_cast<const uint8_t *>(data), static_cast<const uint8_t *>(data) + nbytes);
-  } catch (...) {
-    return gfail(MQ_E_OOM, "GGUF writer: cannot hold %zu bytes of %s", nbytes, name);
-  }
-  w->tensors.push_back(std::move(t));
-  return MQ_OK;
+    w->tensors.push_back(std::move(t));
+    return (int)MQ_OK;
+  });
 }
 
 int mq_gguf_writer_add_qtensor(mq_gguf_writer *w, mq_ctx *ctx, const char *name, const mq_qtensor *qt, int n_dims,
@@ -569,7 +601,6 @@ int mq_gguf_writer_add_qtensor(mq_gguf_writer *w, mq_ctx *ctx, const char *name,
   rc = mq_qtensor_info(qt, &dtype, &n, &k, &gb, nullptr);
   if (rc) return rc;
   WTensor t;
-  t.name = name;
   t.dtype = dtype;
   if (n_dims == 0) {  // [n, k] as GGUF ne = {k, n}
     t.n_dims = 2;
@@ -585,13 +616,24 @@ int mq_gguf_writer_add_qtensor(mq_gguf_writer *w, mq_ctx *ctx, const char *name,
   t.nbytes = gb;
   t.qt = qt;
   t.ctx = ctx;
-  w->tensors.push_back(std::move(t));
-  return MQ_OK;
+  return no_throw("GGUF writer tensor", [&] {
+    t.name = name;
+    w->tensors.push_back(std::move(t));
+    return (int)MQ_OK;
+  });
 }
 
 int mq_gguf_writer_finish(mq_gguf_writer *w) {
   if (!w) return gfail(MQ_E_INVALID, "mq_gguf_writer_finish: NULL writer");
   if (w->finished) return gfail(MQ_E_INVALID, "GGUF writer: already finished");
+  return no_throw("mq_gguf_writer_finish", [&] { return writer_finish(w); });
+}
+
+}  // extern "C"
+
+namespace {
+
+int writer_finish(mq_gguf_writer *w) {
   const std::string tmp = w->path + ".tmp." + std::to_string((long long)getpid());
   FILE *f = fopen(tmp.c_str(), "wb");
   if (!f) return gfail(MQ_E_IO, "cannot create %s", tmp.c_str());
@@ -658,4 +700,4 @@ int mq_gguf_writer_finish(mq_gguf_writer *w) {
   return MQ_OK;
 }
 
-}  // extern "C"
+}  // namespace

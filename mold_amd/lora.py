@@ -105,6 +105,7 @@ class LoraAdapter:
 
     @classmethod
     def load(cls, path: str) -> "LoraAdapter":
+        import torch
         from safetensors.torch import load_file
         tensors = load_file(path, device="cpu")
         a_t, b_t, alpha = {}, {}, {}
@@ -117,10 +118,11 @@ class LoraAdapter:
             elif name.endswith(".lora_B.weight"):
                 b_t[name[:-len(".lora_B.weight")]] = t
             elif name.endswith(".alpha"):
-                try:
-                    alpha[name[:-len(".alpha")]] = float(t.float().reshape(-1)[0]) if t.numel() == 1 else None
-                except Exception:
-                    pass
+                # mold keeps alpha only when `tensor.to_scalar::<f32>()` succeeds
+                # (lora.rs:77-79): a rank-0 F32 tensor.  Any other alpha (bf16 / f16,
+                # or shape [1]) is dropped there, so the effective scale is `scale`.
+                if t.dim() == 0 and t.dtype == torch.float32:
+                    alpha[name[:-len(".alpha")]] = float(t.item())
         layers = {k: LoraLayer(a, b_t[k], alpha.get(k)) for k, a in a_t.items() if k in b_t}
         if not layers:
             raise ValueError(f"no LoRA A/B pairs found in {path}")

@@ -219,6 +219,30 @@ def test_gemv_bias_gelu_strides_bf16(dev, torch):
     assert O.rel_l2(yb, ref_b) <= 1e-2
 
 
+@pytest.mark.parametrize("n,k,m", [(3072, 256, 1), (3072, 256, 3), (640, 768, 1), (9216, 256, 1)])
+def test_gemv_q4k_bf16_x_odd_item_count(dev, torch, n, k, m):
+    """bf16 x staged two items (row of x over one super-block) per direct load: with an
+    odd item count (k = 256 at m = 1: FLUX's time_in / guidance_in linear_1 [3072, 256])
+    the last load must fill only its item.  The result meets the Q8_K bound of the exact
+    product, and repeats bit for bit."""
+    t = GgmlDType.Q4_K
+    _say(f"gemv bf16 x odd items n={n} k={k} m={m}")
+    blocks = _weights(int(t), n, k, seed=n + k + m)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    xb = torch.from_numpy(np.random.default_rng(k * m).standard_normal((m, k)).astype(np.float32)).cuda()
+    xb = xb.to(torch.bfloat16)
+    mm = QMatMul(qt)
+    y1 = mm.forward(xb, out_dtype=torch.float32).clone()
+    y2 = mm.forward(xb, out_dtype=torch.float32).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int32), y2.view(torch.int32))
+    x = xb.float().cpu().numpy()
+    y = y1.cpu().numpy()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    assert np.isfinite(y).all()
+    assert (np.abs(y.astype(np.float64) - ref) <= _q8k_row_bound(x, blocks, int(t), n, k)).all()
+
+
 def test_gemv_q8k_activation_edge_cases(dev, torch):
     """Q8_K staging of the Q4_K GEMV on awkward activations: ties in |x| with opposite
     signs, all-zero super-blocks (d = 0), a lone non-zero element, a constant block (every

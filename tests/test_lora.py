@@ -89,3 +89,32 @@ def test_oracle_lora_apply_f64_bound():
     ref = w.astype(np.float64) + 0.75 * (b.astype(np.float64) @ a.astype(np.float64))
     bound = 4 * 2.0 ** -24 * (np.abs(w) + 0.75 * (np.abs(b) @ np.abs(a)) * 48)
     assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_adapter_alpha_only_from_rank0_f32(tmp_path):
+    """LoraAdapter::load keeps `<layer>.alpha` only when `to_scalar::<f32>()`
+    succeeds (lora.rs:77-79), i.e. for a rank-0 F32 tensor; a bf16 / f16 alpha or
+    a shape-[1] alpha is dropped, so those layers use the plain scale."""
+    torch = pytest.importorskip("torch")
+    from safetensors.torch import save_file
+    from mold_amd.lora import LoraAdapter, build_patches
+    st = {}
+    cases = {"f32_rank0": (torch.tensor(8.0), 8.0), "bf16_rank0": (torch.tensor(8.0, dtype=torch.bfloat16), None),
+             "f16_rank0": (torch.tensor(8.0, dtype=torch.float16), None), "f32_shape1": (torch.tensor([8.0]), None)}
+    for i, (nm, (alpha, _)) in enumerate(cases.items()):
+        key = f"transformer.single_transformer_blocks.{i}.proj_out"
+        st[f"{key}.lora_A.weight"] = torch.ones((4, 16))
+        st[f"{key}.lora_B.weight"] = torch.ones((16, 4))
+        st[f"{key}.alpha"] = alpha
+    path = tmp_path / "lora.safetensors"
+    save_file(st, str(path))
+    ad = LoraAdapter.load(str(path))
+    for i, (nm, (_, want)) in enumerate(cases.items()):
+        layer = ad.layers[f"transformer.single_transformer_blocks.{i}.proj_out"]
+        assert layer.alpha == want, nm
+    patches, skipped = build_patches(ad, 0.5)
+    assert skipped == 0
+    effs = {p.target.candle_key: p.effective_scale for pl in patches.values() for p in pl}
+    assert effs["single_blocks.0.linear2.weight"] == 0.5 * 8.0 / 4     # scale * alpha / rank
+    for i in (1, 2, 3):
+        assert effs[f"single_blocks.{i}.linear2.weight"] == 0.5       # alpha dropped
