@@ -17,13 +17,23 @@
  *   quantize_row_*_ref ....... ggml-quants.c  (llama-quantize without imatrix)
  *   vec_dot_*_q8_* ........... ggml-quants.c generic paths (candle: `vec_dot_unopt`)
  *   Q8_1 / Q8_K activations .. candle k_quants.rs `from_float` as recalled
- *                              (round-half-away, Q8_K scale -128/max; ggml
- *                              differs in last bits).  PARITY UNPINNED: no
- *                              candle source or vectors exist here, so tests
- *                              report agreement with it but assert only
- *                              convention-independent bounds.
+ *                              (round-half-away, Q8_K scale -128/max; ggml's
+ *                              quantize_row_q8_K_ref uses -127/max and ties to
+ *                              even).  The code is pinned to that stated
+ *                              convention (known-answer rows that separate the
+ *                              two, a second numpy restatement); whether candle
+ *                              rounds this way is PARITY UNPINNED: no candle
+ *                              source or vectors exist here, so GPU tests report
+ *                              agreement with it but assert only bounds that
+ *                              hold for either convention.
  *   matmul ................... candle quantized/mod.rs `matmul_t`: quantize each
  *                              activation row, then vec_dot per output column.
+ * How each part is pinned (tests/test_oracle.py): dequantize by known-answer
+ * blocks, a numpy restatement and the once-rounded exact value; the reference
+ * quantizers by known-answer rows (legacy types), a numpy restatement
+ * (oracle/np_quant.py, byte for byte) and exact round trips on each format's
+ * grid; vec_dot by the exact product to f32 rounding; matmul_candle as
+ * quantized rows times vec_dot; matmul_f64 by numpy BLAS.
  * Call sites in the reference that reach these: QTensor::dequantize at
  * crates/mold-inference/src/qwen_image/quantized_transformer.rs:62-66 and
  * crates/mold-inference/src/flux/lora.rs:765; QMatMul::forward through

@@ -8,6 +8,22 @@ it and fails loudly when its own HIP library is missing.
 The restated algorithms (ggml block formats and reference quantizers, candle's
 CPU QMatMul) and the reference call sites they stand for are listed in the
 header of ``ggml_oracle.c``.
+
+Pins of every function here (tests/test_oracle.py unless noted):
+  block_size / type_size ..... ggml's type table and the reference's GGUF file sizes
+  quantize ................... known-answer rows (legacy types), byte identity with
+                               oracle/np_quant.py, exact round trips on each grid
+  dequantize ................. known-answer blocks, oracle/np_dequant.py, the
+                               once-rounded exact value
+  quantize_act ............... known-answer rows, byte identity with np_quant
+  vec_dot .................... the exact product to f32 rounding
+  matmul_candle .............. quantized rows x vec_dot, bit for bit; 1e-2 of f64
+  matmul_f64 ................. numpy float64 BLAS, linearity, zero blocks
+  e4m3_to_f32 ................ every byte against torch.float8_e4m3fn
+                               (tests/test_gguf_format.py)
+  lora_apply ................. exact cases and an f64 bound (tests/test_lora.py)
+Parity unpinned: candle's own Q8_K / Q8_1 rounding convention (``quantize_act``
+follows the stated one; no assertion on the GPU depends on it).
 """
 from __future__ import annotations
 
