@@ -10,6 +10,13 @@
  *   - A weight is a GGUF tensor of `n` rows (output features) by `k` columns
  *     (input features, GGUF ne[0]); each row is k/block_size consecutive
  *     blocks.  The layer computes y[m, n] = x[m, k] . W[n, k]^T (+ bias[n]).
+ *   - Dense GGUF tensors (MQ_F32 / MQ_F16 / MQ_BF16: biases, norm scales,
+ *     embeddings) are mq_qtensors too, as candle's QTensor holds them: n rows
+ *     of k elements (a 1-D tensor is n = 1), stored row-major as in the file.
+ *     They upload, download, load from GGUF files and dequantize (convert)
+ *     like the block types; a quantized matmul refuses them
+ *     (MQ_E_UNSUPPORTED), since candle's QMatMul::from_arc dequantizes a
+ *     dense weight once and runs a dense matmul instead.
  *   - Return value 0 is success; a negative MQ_E_* code is failure and
  *     mq_last_error() returns a thread-local message.  Nothing aborts or
  *     throws across the ABI.
@@ -100,7 +107,8 @@ int mq_ctx_set_stream_tail_split(mq_ctx *ctx, void *stream, int enabled);
 int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int64_t m, int gated,
                               size_t *bytes);
 
-/* Upload a GGUF weight (blocks exactly as stored in the file) to the device.
+/* Upload a GGUF tensor (blocks, or dense elements, exactly as stored in the
+ * file) to the device.
  * Replaces QCudaStorage load_quantized / `content.tensor(reader, name, device)`
  * (crates/mold-inference/src/flux/lora.rs:722) and VarBuilder::from_gguf
  * (crates/mold-inference/src/flux/pipeline.rs:976).  Synchronous: the host
@@ -123,7 +131,10 @@ int mq_qtensor_from_device(mq_ctx *ctx, int dtype, int64_t n, int64_t k,
  * QTensor::quantize / quantize_onto (crates/mold-inference/src/flux/
  * pipeline.rs:219-229, crates/mold-inference/src/flux/lora.rs:849).
  * Runs on `stream` after work already queued there and returns when the
- * blocks are in place (through the context's upload staging buffer). */
+ * blocks are in place (through the context's upload staging buffer).
+ * dtype F32 / F16 / BF16 stores the values themselves (rounded to nearest
+ * even when narrowing): QTensor::quantize(.., F32), which mold uses for the
+ * tensors a block type cannot hold (flux/pipeline.rs:223-228). */
 int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, int64_t ld,
                 void *stream, mq_qtensor **out);
 /* Same from FP8 E4M3 weights already on the device: src[n, ld] bytes in the
@@ -134,7 +145,7 @@ int mq_quantize(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const float *src, 
  * pipeline.rs:120-252, which loads the FP8 tensor and calls
  * QTensor::quantize(.., Q8_0) at :212-216).  Synchronous like mq_quantize. */
 int mq_quantize_fp8(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *src, int64_t ld,
-                    float scale, void *stream, mq_qtensor **out);
+                    float scale, void *stream, mq_qtensor **out);  /* block types only */
 /* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
  * Synchronous. */
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes);
@@ -145,7 +156,11 @@ int mq_qtensor_info(const mq_qtensor *w, int *dtype, int64_t *n, int64_t *k,
 
 /* QTensor::dequantize(&device) -> dense [n, k] in dst_dtype (F32, F16 or
  * BF16) at dst (row-major, k contiguous).  F32 output is bit-exact with the
- * GGUF formulas; F16/BF16 are that value rounded to nearest even.
+ * GGUF formulas; F16/BF16 are that value rounded to nearest even.  A dense
+ * tensor converts: the same type is a copy, widening is exact, narrowing
+ * rounds to nearest even (candle's dequantize of F32 / F16 tensors,
+ * crates/mold-inference/src/qwen_image/quantized_transformer.rs:83-86,
+ * crates/mold-inference/src/flux2/quantized_transformer.rs:49-54).
  * Replaces candle's dequantize / dequantize_f16 (called at
  * crates/mold-inference/src/qwen_image/quantized_transformer.rs:62-66). */
 int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, void *stream);
@@ -229,10 +244,12 @@ int64_t mq_gguf_find(const mq_gguf *g, const char *name);
 /* dims[0] is GGUF ne[0] (the contiguous axis). *name stays valid until close. */
 int mq_gguf_tensor_info(const mq_gguf *g, int64_t index, const char **name, int *dtype,
                         int *n_dims, int64_t dims[4], uint64_t *file_offset, size_t *nbytes);
-/* Read a 2-D quantized tensor from the file and upload it (content.tensor(
- * reader, name, device)): the file is read in 16 MiB chunks into two pinned
- * host buffers in turn, each copied to the device asynchronously while the
- * next is read, then repacked on the device.  Synchronous. */
+/* Read a tensor from the file and upload it (content.tensor(reader, name,
+ * device), crates/mold-inference/src/flux/lora.rs:721-723): rows = the
+ * product of ne[1..], k = ne[0]; block types and dense F32 / F16 / BF16.  The
+ * file is read in 16 MiB chunks into two pinned host buffers in turn, each
+ * copied to the device asynchronously while the next is read, then repacked
+ * on the device (block types).  Synchronous. */
 int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out);
 /* The tensor's raw bytes as stored (any type, dense F32/F16/BF16 included)
  * into host memory; nbytes must equal the tensor's size.  What mold reads

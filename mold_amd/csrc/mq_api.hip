@@ -106,20 +106,28 @@ constexpr size_t kMiB = size_t(1) << 20;
 size_t round_mib(size_t b) { return (b + kMiB - 1) & ~(kMiB - 1); }
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// Dense GGUF tensors (biases, norm scales, embeddings and other tensors a
+// block type cannot hold) are stored as they are in the file: row-major [n, k].
+bool is_dense(int dtype) { return dtype == MQ_F32 || dtype == MQ_F16 || dtype == MQ_BF16; }
+size_t dense_size(int dtype) { return dtype == MQ_F32 ? 4 : 2; }
+const char *dense_name(int dtype) { return dtype == MQ_F32 ? "F32" : dtype == MQ_F16 ? "F16" : "BF16"; }
+
 size_t gguf_row_bytes(int dtype, int64_t k) {
+  if (is_dense(dtype)) return (size_t)k * dense_size(dtype);
   const TypeInfo ti = type_info(dtype);
   return (size_t)(k / ti.bs) * ti.ts;
 }
 
 int check_weight_shape(int dtype, int64_t n, int64_t k, size_t nbytes) {
-  if (!is_quant(dtype)) return fail(MQ_E_INVALID, "dtype %d is not a supported GGUF block type", dtype);
-  const TypeInfo ti = type_info(dtype);
+  if (!is_quant(dtype) && !is_dense(dtype))
+    return fail(MQ_E_INVALID, "dtype %d is not a GGUF block type or F32 / F16 / BF16", dtype);
+  const char *name = is_dense(dtype) ? dense_name(dtype) : type_info(dtype).name;
   if (n <= 0 || k <= 0) return fail(MQ_E_INVALID, "weight shape [%lld, %lld] must be positive", (long long)n, (long long)k);
-  if (k % ti.bs != 0)
-    return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", ti.name, ti.bs, (long long)k);
+  if (!is_dense(dtype) && k % type_info(dtype).bs != 0)
+    return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", name, type_info(dtype).bs, (long long)k);
   const size_t want = gguf_row_bytes(dtype, k) * (size_t)n;
   if (nbytes != want)
-    return fail(MQ_E_INVALID, "%s [%lld, %lld] is %zu bytes, got %zu", ti.name, (long long)n, (long long)k, want, nbytes);
+    return fail(MQ_E_INVALID, "%s [%lld, %lld] is %zu bytes, got %zu", name, (long long)n, (long long)k, want, nbytes);
   return MQ_OK;
 }
 
@@ -263,6 +271,11 @@ int check_qmatmul_args(const char *fn, const mq_ctx *ctx, const mq_qtensor *w, c
   if (m < 0) return fail(MQ_E_INVALID, "%s: m=%lld < 0", fn, (long long)m);
   if (m == 0) return MQ_OK;
   if (!x || !y) return fail(MQ_E_INVALID, "%s: NULL x or y", fn);
+  if (is_dense(w->dtype))
+    return fail(MQ_E_UNSUPPORTED,
+                "%s: the weight is a dense %s tensor; like candle's QMatMul::from_arc, dequantize it once "
+                "(mq_dequantize) and use the device's dense matmul",
+                fn, dense_name(w->dtype));
   if (x_dtype != MQ_F32 && x_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: x dtype %d must be F32 or BF16", fn, x_dtype);
   if (y_dtype != MQ_F32 && y_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: y dtype %d must be F32 or BF16", fn, y_dtype);
   if (ldx < w->k) return fail(MQ_E_INVALID, "%s: ldx=%lld < k=%lld", fn, (long long)ldx, (long long)w->k);
@@ -278,8 +291,16 @@ int make_tensor(mq_ctx *ctx, int dtype, int64_t n, int64_t k, mq_qtensor **out) 
   t->dtype = dtype;
   t->n = n;
   t->k = k;
-  t->geo = make_geo(dtype, n, k);
   t->gguf_bytes = gguf_row_bytes(dtype, k) * (size_t)n;
+  if (is_dense(dtype)) {  // stored as in the file: no tiles, no planes
+    t->geo = Geo{};
+    t->geo.n = n;
+    t->geo.k = k;
+    t->geo.nb = k;
+    t->geo.bytes = (int64_t)t->gguf_bytes;
+  } else {
+    t->geo = make_geo(dtype, n, k);
+  }
   int rc = alloc_weight(ctx, t);
   if (rc != MQ_OK) {
     delete t;
@@ -296,7 +317,8 @@ int tensor_from_raw(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *ra
   mq_qtensor *t = nullptr;
   int rc = make_tensor(ctx, dtype, n, k, &t);
   if (rc) return rc;
-  hipError_t e = launch_repack(dtype, raw, t->data, t->geo, false, s);
+  hipError_t e = is_dense(dtype) ? hipMemcpyAsync(t->data, raw, t->gguf_bytes, hipMemcpyDeviceToDevice, s)
+                                 : launch_repack(dtype, raw, t->data, t->geo, false, s);
   if (e != hipSuccess) {
     mq_qtensor_free(t);
     return hip_fail(e, "repack to device layout");
@@ -453,6 +475,18 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
   int rc = check_weight_shape(dtype, n, k, nbytes);
   if (rc) return rc;
   DeviceGuard g(ctx->device);
+  if (is_dense(dtype)) {  // no repack: the bytes go straight to their place
+    mq_qtensor *t = nullptr;
+    rc = make_tensor(ctx, dtype, n, k, &t);
+    if (rc) return rc;
+    const hipError_t e = hipMemcpy(t->data, host_blocks, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      mq_qtensor_free(t);
+      return hip_fail(e, "hipMemcpy H2D");
+    }
+    *out = t;
+    return MQ_OK;
+  }
   uint8_t *st = nullptr;
   rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;
@@ -474,9 +508,28 @@ static int quantize_common(mq_ctx *ctx, const char *fn, int dtype, int64_t n, in
                            int64_t ld, float scale, void *stream, mq_qtensor **out) {
   if (!ctx || !out || !src) return fail(MQ_E_INVALID, "%s: NULL argument", fn);
   *out = nullptr;
-  if (!is_quant(dtype)) return fail(MQ_E_INVALID, "%s: dtype %d is not a GGUF block type", fn, dtype);
   if (n <= 0 || k <= 0 || ld < k)
     return fail(MQ_E_INVALID, "%s: bad shape n=%lld k=%lld ld=%lld", fn, (long long)n, (long long)k, (long long)ld);
+  if (is_dense(dtype) && !fp8) {
+    // QTensor::quantize(.., F32 / F16 / BF16): the values themselves, rounded to
+    // nearest even when narrowing (mold stores its small tensors this way,
+    // flux/pipeline.rs:223-228)
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    mq_qtensor *t = nullptr;
+    int rc = make_tensor(ctx, dtype, n, k, &t);
+    if (rc) return rc;
+    hipError_t e = launch_convert(src, MQ_F32, ld, n, k, t->data, dtype, k, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      mq_qtensor_free(t);
+      return hip_fail(e, "dense quantize");
+    }
+    *out = t;
+    return MQ_OK;
+  }
+  if (!is_quant(dtype))
+    return fail(MQ_E_INVALID, "%s: dtype %d is not a GGUF block type%s", fn, dtype, fp8 ? "" : " or F32 / F16 / BF16");
   const TypeInfo ti = type_info(dtype);
   if (k % ti.bs != 0) return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", ti.name, ti.bs, (long long)k);
   DeviceGuard g(ctx->device);
@@ -513,6 +566,10 @@ int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, siz
   if (!ctx || !w || !host_blocks) return fail(MQ_E_INVALID, "mq_qtensor_download: NULL argument");
   if (nbytes != w->gguf_bytes) return fail(MQ_E_INVALID, "download needs %zu bytes, got %zu", w->gguf_bytes, nbytes);
   DeviceGuard g(ctx->device);
+  if (is_dense(w->dtype)) {
+    HIP_TRY(hipMemcpy(host_blocks, w->data, nbytes, hipMemcpyDeviceToHost), "download");
+    return MQ_OK;
+  }
   uint8_t *st = nullptr;
   int rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;
@@ -549,7 +606,15 @@ int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, vo
     return fail(MQ_E_INVALID, "mq_dequantize: dst dtype %d must be F32, F16 or BF16", dst_dtype);
   if (reinterpret_cast<uintptr_t>(dst) & 15) return fail(MQ_E_INVALID, "mq_dequantize: dst must be 16-byte aligned");
   DeviceGuard g(ctx->device);
-  hipError_t e = launch_dequant(w->dtype, view_of(w), w->n, w->k, dst, dst_dtype, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (is_dense(w->dtype)) {
+    const hipError_t e = w->dtype == dst_dtype
+                             ? hipMemcpyAsync(dst, w->data, w->gguf_bytes, hipMemcpyDeviceToDevice, s)
+                             : launch_convert(w->data, w->dtype, w->k, w->n, w->k, dst, dst_dtype, w->k, s);
+    if (e != hipSuccess) return hip_fail(e, "dense dequantize");
+    return MQ_OK;
+  }
+  hipError_t e = launch_dequant(w->dtype, view_of(w), w->n, w->k, dst, dst_dtype, s);
   if (e != hipSuccess) return hip_fail(e, "dequantize launch");
   return MQ_OK;
 }
@@ -559,6 +624,9 @@ int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int
   if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: m=%lld < 0", (long long)m);
   if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
     return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: x dtype %d must be F32 or BF16", x_dtype);
+  if (is_dense(w->dtype))
+    return fail(MQ_E_UNSUPPORTED, "mq_qmatmul_workspace_size: dense %s weights take no quantized matmul",
+                dense_name(w->dtype));
   // a misaligned x pointer takes every staging path, so this is the bound
   // over all x placements and strides
   const void *worst = reinterpret_cast<const void *>(uintptr_t(1));

@@ -411,8 +411,6 @@ int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor
   if (!g || !out || index < 0 || index >= (int64_t)g->tensors.size())
     return gfail(MQ_E_INVALID, "mq_gguf_load_tensor: bad argument");
   const TensorInfo &t = g->tensors[(size_t)index];
-  if (mq_block_size(t.dtype) <= 1)
-    return gfail(MQ_E_UNSUPPORTED, "tensor %s is dense (type %d); only GGUF block types upload", t.name.c_str(), t.dtype);
   int64_t rows = 1;
   for (int d = 1; d < t.n_dims; ++d) rows *= t.dims[d];
   if (!ctx) return gfail(MQ_E_INVALID, "mq_gguf_load_tensor: NULL ctx");

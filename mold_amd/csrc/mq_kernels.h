@@ -20,6 +20,11 @@ hipError_t launch_quantize_fp8(int type, const uint8_t *src, int64_t ld, int64_t
                                void *dst_raw, hipStream_t stream);
 hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
                           hipStream_t stream);
+// Dense GGUF tensors (F32 / F16 / BF16): src[n, lds] of src_type -> dst[n,
+// ldd] of dst_type, element by element: widening is exact, narrowing rounds
+// to nearest even (NaN stays NaN).  Same type: a plain copy is cheaper.
+hipError_t launch_convert(const void *src, int src_type, int64_t lds, int64_t n, int64_t k, void *dst,
+                          int dst_type, int64_t ldd, hipStream_t stream);
 // bf16 [m, k] (row stride ldx) -> f32 [m, k] contiguous, for the GEMV.
 hipError_t launch_widen_bf16(const __bf16 *x, int64_t m, int64_t k, int64_t ldx, float *out,
                              hipStream_t stream);

@@ -200,6 +200,66 @@ hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *
   return hipGetLastError();
 }
 
+// ------------------------------------------------------- dense GGUF tensors
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return (float)v;  // exact from f16 and bf16
+}
+
+template <typename OUT>
+__device__ __forceinline__ OUT from_f32(float v) {
+  return (OUT)v;  // f32 -> f16 / bf16: round to nearest even
+}
+
+// One thread per 4 consecutive elements of a row (grid-stride over rows x
+// column groups); the last group of a row may be partial.
+template <typename IN, typename OUT>
+__global__ __launch_bounds__(256) void convert_kernel(const IN *__restrict__ src, int64_t lds, int64_t n, int64_t k,
+                                                      OUT *__restrict__ dst, int64_t ldd) {
+  const int64_t gpr = (k + 3) >> 2;
+  const int64_t total = n * gpr;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / gpr;
+    const int64_t c0 = (i - row * gpr) << 2;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c0 + j < k) dst[row * ldd + c0 + j] = from_f32<OUT>(to_f32(src[row * lds + c0 + j]));
+  }
+}
+
+template <typename IN>
+static hipError_t convert_from(const IN *src, int64_t lds, int64_t n, int64_t k, void *dst, int dst_type,
+                               int64_t ldd, hipStream_t stream) {
+  const int64_t total = n * ((k + 3) >> 2);
+  const int64_t want = (total + 255) / 256;
+  const int blocks = (int)(want < 65536 ? want : 65536);
+  if (dst_type == F32)
+    hipLaunchKernelGGL((convert_kernel<IN, float>), dim3(blocks), dim3(256), 0, stream, src, lds, n, k,
+                       static_cast<float *>(dst), ldd);
+  else if (dst_type == F16)
+    hipLaunchKernelGGL((convert_kernel<IN, _Float16>), dim3(blocks), dim3(256), 0, stream, src, lds, n, k,
+                       static_cast<_Float16 *>(dst), ldd);
+  else if (dst_type == BF16)
+    hipLaunchKernelGGL((convert_kernel<IN, __bf16>), dim3(blocks), dim3(256), 0, stream, src, lds, n, k,
+                       static_cast<__bf16 *>(dst), ldd);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_convert(const void *src, int src_type, int64_t lds, int64_t n, int64_t k, void *dst,
+                          int dst_type, int64_t ldd, hipStream_t stream) {
+  if (n <= 0 || k <= 0) return hipSuccess;
+  switch (src_type) {
+    case F32: return convert_from(static_cast<const float *>(src), lds, n, k, dst, dst_type, ldd, stream);
+    case F16: return convert_from(static_cast<const _Float16 *>(src), lds, n, k, dst, dst_type, ldd, stream);
+    case BF16: return convert_from(static_cast<const __bf16 *>(src), lds, n, k, dst, dst_type, ldd, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // ------------------------------------------------- activation staging (GEMM A)
 
 // x[m, k] (f32 or bf16, row stride ldx) -> bf16 [m, kp] with zeros in

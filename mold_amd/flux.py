@@ -46,6 +46,8 @@ import math
 from dataclasses import dataclass
 from typing import Callable, Dict, Optional, Tuple
 
+import numpy as np
+
 from .quantized import ACT_GELU_TANH, ACT_NONE, GgmlDType, Linear, QTensor
 
 
@@ -159,6 +161,44 @@ class FluxParams:
             elif name == "img_in.weight":
                 t = t.to(torch.bfloat16)
             dense[name] = t
+        return FluxParams(cfg, lin, dense)
+
+    @staticmethod
+    def from_gguf(cfg: FluxConfig, path: str, device) -> "FluxParams":
+        """The transformer's parameters from a GGUF file in mold's layout (candle's
+        FLUX tensor names, `<linear>.weight` / `<linear>.bias`, norm `.scale`s,
+        `img_in`), loaded the way mold's `VarBuilder::from_gguf` does
+        (crates/mold-inference/src/flux/pipeline.rs:976-977): every tensor goes to
+        the device through libmoldq (mq_gguf_load_tensor), block-type weights stay
+        quantized, and dense tensors (F32 / F16 / BF16) are dequantized on the
+        device to the dtypes the step uses (f32 biases, bf16 norm scales and
+        img_in weight).  No tensor byte passes through the host here except on
+        the upload itself."""
+        import torch
+        from . import gguf
+        c = gguf.Content.read(path)
+        try:
+            def load(name, shape):
+                if name not in c.tensor_infos:
+                    raise KeyError(f"{path}: tensor {name} missing")
+                qt = c.tensor(name, device)
+                want = (int(np.prod(shape[:-1])) if len(shape) > 1 else 1, shape[-1])
+                if qt.shape != want:
+                    raise ValueError(f"{name}: stored as {qt.shape}, the config needs {tuple(shape)}")
+                return qt
+
+            lin, dense = {}, {}
+            for name, (n, k, has_bias) in linear_shapes(cfg).items():
+                qt = load(name + ".weight", (n, k))
+                if not qt.dtype().is_quantized:
+                    raise ValueError(f"{name}.weight is dense {qt.dtype().name}; the step runs quantized linears")
+                bias = load(name + ".bias", (n,)).dequantize(torch.float32).reshape(n) if has_bias else None
+                lin[name] = Linear(qt, bias)
+            for name, shape in dense_shapes(cfg).items():
+                dt = torch.float32 if name.endswith(".bias") else torch.bfloat16
+                dense[name] = load(name, shape).dequantize(dt).reshape(shape)
+        finally:
+            c.close()
         return FluxParams(cfg, lin, dense)
 
     def quantized_bytes(self) -> int:

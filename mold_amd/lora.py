@@ -191,44 +191,24 @@ def patch_qtensor(qt: QTensor, patches: List[LoraPatch]) -> Tuple[QTensor, int]:
 
 def gguf_lora_var_builder(transformer_path: str, adapter: LoraAdapter, scale: float, device: Device):
     """gguf_lora_var_builder (lora.rs:661-869) with the patching on the GPU.
-    Returns ({name: QTensor for quantized tensors, torch tensor for dense
-    ones}, applied patch count).  Targeted dense tensors are patched with
-    torch in f32."""
-    import torch
+    Every tensor of the file is loaded to the device as a QTensor
+    (content.tensor(.., device), lora.rs:721-723), dense F32 / F16 / BF16 ones
+    included; each targeted tensor is dequantized to f32, patched and
+    re-quantized to its own type (quantize_onto, :849), as mold does.
+    Returns ({name: QTensor}, applied patch count): the tensor set that mold
+    hands to VarBuilder::from_qtensors (:868)."""
     from . import gguf
     patches, _ = build_patches(adapter, scale)
     c = gguf.Content.read(transformer_path)
-    data: Dict[str, object] = {}
+    data: Dict[str, QTensor] = {}
     try:
-        for name, info in c.tensor_infos.items():
-            if info.dtype in (GgmlDType.F32, GgmlDType.F16, GgmlDType.BF16):
-                np_dt = {GgmlDType.F32: "float32", GgmlDType.F16: "float16", GgmlDType.BF16: None}[info.dtype]
-                raw = torch.from_numpy(c.tensor_bytes(name))
-                t = raw.view(torch.bfloat16) if np_dt is None else raw.view(getattr(torch, np_dt))
-                data[name] = t.reshape(info.shape).to(f"cuda:{device.ordinal}")
-            else:
-                data[name] = c.tensor(name, device)
+        for name in c.tensor_infos:
+            data[name] = c.tensor(name, device)
     finally:
         c.close()
     applied = 0
     for key, plist in patches.items():
-        if key not in data:
-            continue
-        cur = data[key]
-        if isinstance(cur, QTensor):
-            data[key], n = patch_qtensor(cur, plist)
+        if key in data:
+            data[key], n = patch_qtensor(data[key], plist)
             applied += n
-        else:
-            t = cur.float().reshape(cur.shape[0], -1).clone()
-            for p in plist:
-                rows = slice(None)
-                if p.target.fused:
-                    off, size = fused_slice_range(t.shape[0], p.b.shape[0], p.target.component,
-                                                  p.target.num_components)
-                    if off + size > t.shape[0]:
-                        continue
-                    rows = slice(off, off + size)
-                lora_apply(t[rows], p.b, p.a, p.effective_scale)
-                applied += 1
-            data[key] = t.reshape(cur.shape).to(cur.dtype)
     return data, applied

@@ -226,3 +226,64 @@ def test_flux_step_tiny_matches_dequantized_reference():
     params.lin[nm] = old
     assert step._mod_stack is not stack_before
     assert torch.equal(out2, out2_sep) and not torch.equal(out2, out)
+
+
+@pytest.mark.gpu
+def test_flux_step_from_mold_layout_gguf(tmp_path):
+    """A tiny-config FLUX GGUF in mold's layout, written by an independent
+    restatement of the container (tests/gguf_ref.py): Q4_K linear weights, F32
+    biases and norm scales, an F16 img_in weight (K = 64 holds no 256-wide
+    super-block), candle's tensor names, GGUF ne order.  FluxParams.from_gguf loads
+    it through the C ABI alone (mq_gguf_load_tensor for every tensor, dense ones
+    dequantized on the device; no host read of tensor bytes), and the step
+    matches the f64 restatement on the file's own values within the 1e-2 bar."""
+    import mold_amd
+    from oracle import oracle as O
+    from . import gguf_ref as R
+    cfg = F.FluxConfig.tiny()
+    print("[flux] tiny step from a mold-layout GGUF", flush=True)
+    rng = np.random.default_rng(12)
+    tensors, W, D = [], {}, {}
+    for name, (n, k, hb) in F.linear_shapes(cfg).items():
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        blocks = O.quantize(O.Q4_K, w)
+        tensors.append((name + ".weight", O.Q4_K, (n, k), blocks))
+        b = None
+        if hb:
+            b = (rng.standard_normal(n) * 0.02).astype(np.float32)
+            tensors.append((name + ".bias", O.F32, (n,), b.view(np.uint8)))
+        W[name] = (torch.from_numpy(O.dequantize(O.Q4_K, blocks, n, k)), None if b is None else torch.from_numpy(b))
+    for name, shape in F.dense_shapes(cfg).items():
+        v = rng.standard_normal(shape).astype(np.float32) * 0.02
+        if name.endswith(".scale"):
+            v = v + 1.0
+        if name == "img_in.weight":
+            h16 = v.astype(np.float16)
+            tensors.append((name, O.F16, shape, h16.view(np.uint8)))
+            D[name] = torch.from_numpy(h16.astype(np.float32))
+        else:
+            tensors.append((name, O.F32, shape, v.view(np.uint8)))
+            D[name] = torch.from_numpy(v)
+    path = str(tmp_path / "flux-tiny-q4_k.gguf")
+    R.write(path, [("general.architecture", 8, "flux")], tensors)
+    dev = mold_amd.Device(0)
+    params = F.FluxParams.from_gguf(cfg, path, dev)
+    # what the device holds is what the file holds (dense values converted exactly as
+    # torch converts them; weights byte-identical)
+    for name, (n, k, hb) in F.linear_shapes(cfg).items():
+        qt = params.lin[name].matmul.w
+        assert qt.dtype() == mold_amd.GgmlDType.Q4_K and qt.shape == (n, k)
+        if hb:
+            assert torch.equal(params.lin[name].bias.cpu(), W[name][1])
+    for name, t in D.items():
+        want = t if name.endswith(".bias") else t.to(torch.bfloat16)
+        assert torch.equal(params.dense[name].cpu(), want), name
+    inp = F.make_inputs(cfg, height=256, width=256, txt_len=32, device="cuda", seed=13)
+    out = F.FluxStep(params).forward(**inp)
+    torch.cuda.synchronize()
+    ref = reference_forward(cfg, W, D, {k_: v.cpu() for k_, v in inp.items()})
+    o = out.cpu().numpy()
+    assert np.isfinite(o).all()
+    err = _rel(o, ref.numpy())
+    print(f"[flux] GGUF-loaded step rel-L2 vs f64 reference: {err:.3e}", flush=True)
+    assert err <= STEP_TOL, err

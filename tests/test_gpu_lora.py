@@ -141,5 +141,7 @@ def test_gguf_lora_var_builder(dev, torch, tmp_path):
         else:
             ref = blocks[nm].reshape(-1)
         assert np.array_equal(got.data(), ref), nm
-    nrm = data["double_blocks.0.img_attn.norm.query_norm.scale"]
-    assert np.array_equal(nrm.cpu().numpy(), norm)
+    nrm = data["double_blocks.0.img_attn.norm.query_norm.scale"]      # a dense F32 tensor, untouched
+    assert isinstance(nrm, QTensor) and nrm.dtype() == GgmlDType.F32 and nrm.shape == (1, 128)
+    assert np.array_equal(nrm.data(), norm.view(np.uint8))
+    assert np.array_equal(nrm.dequantize().cpu().numpy().reshape(-1), norm)
