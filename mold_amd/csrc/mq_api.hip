@@ -188,7 +188,7 @@ struct Plan {
   bool stage_gemm = false;  // f32 (or unaligned bf16) x staged as bf16 for the GEMM
   bool stage_gemv = false;  // x widened / copied to contiguous f32 for the generic GEMV
   int64_t kp = 0;           // staged GEMM row length (k rounded up to 64)
-  GemmTail tail{0, 1};
+  GemmTail tail{0, 1, kGemmTileM};
   size_t stage_off = 0, stage_bytes = 0;
   size_t part_off = 0, part_bytes = 0;  // GEMM tail partials or generic-GEMV K-split partials
   size_t total = 0;
@@ -210,7 +210,7 @@ Plan plan_qmatmul(const mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_d
         !(x_dtype == MQ_BF16 && k == p.kp && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0);
     const int64_t lda = p.stage_gemm ? p.kp : ldx;
     p.stage_bytes = p.stage_gemm ? (size_t)m * p.kp * sizeof(__bf16) : 0;
-    if (tail_split) p.tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count);
+    p.tail = gemm_tail_plan(w->dtype, m, n, k, ctx->cu_count, tail_split);
     if (p.tail.kparts > 1 && gemm_fast_ok(w->dtype, m, k, lda)) p.part_bytes = gemm_tail_bytes(p.tail, m, n);
     else p.tail.kparts = 1;
   }

@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
 
 // ---------------------------------------------------------------------------
 // Fast path.  Block tile kFM x kFN, K step kFK; see the file comment.
-constexpr int kFM = kGemmTileM, kFN = kGemmTileN, kFK = 64;
+constexpr int kFN = kGemmTileN, kFK = 64;
 constexpr int kFastThreads = 256;
 constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
 constexpr int MQ_ACT_GELU_ = 1;  // mq_act MQ_ACT_GELU_TANH (the only other value)
@@ -257,13 +257,14 @@ __device__ __forceinline__ void step_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <int TYPE, typename OUT, bool GATED>
+template <int TYPE, typename OUT, bool GATED, int kFM>
 __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
     OUT *y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate, int act, int tiles_m,
     int tiles_n, int full_tiles, int kparts, float *__restrict__ partial) {
   using TT = bfrag::T<TYPE>;
   constexpr int kP = TT::kUnitK / kFK;  // K steps per weight unit
+  constexpr int kMB = kFM / 32;         // 32-row MFMA blocks of the tile
   __shared__ uint4 lds_a[2][kFM * kFK / 8];
 
   // Workgroups 0 .. full_tiles-1 run whole tiles (XCD-aware order over
@@ -297,13 +298,13 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   const int64_t units = part < 0 ? all_units : (part + 1) * all_units / kparts - ub;
   const int64_t ksteps = units * kP;
 
-  f32x16 acc[8];
+  f32x16 acc[kMB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kMB; ++i)
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[i][e] = 0.f;
 
-  // A staging by LDS DMA: load i (0..7) of wave `wave` fills LDS rows
+  // A staging by LDS DMA: load i (0 .. kMB-1) of wave `wave` fills LDS rows
   // 32 i + 8 wave .. +7 of a slot (1 KiB), lane -> row ar = tid / 8, LDS
   // chunk slot ac = tid % 8, so the lane fetches global chunk
   // ac ^ ((ar >> 1) & 7) ((ar + 32 i) >> 1 & 7 == ar >> 1 & 7).  Rows past m
@@ -312,9 +313,9 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   // uniform base address.
   const int ac = tid & 7, ar = tid >> 3;
   const int gch = ac ^ ((ar >> 1) & 7);
-  uint32_t voff[8];
+  uint32_t voff[kMB];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kMB; ++i) {
     const int64_t r = m0 + ar + 32 * i < m ? m0 + ar + 32 * i : m - 1;
     voff[i] = (uint32_t)((r * lda + gch * 8) * 2);
   }
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     const char *sb = reinterpret_cast<const char *>(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32)) << 32) |
                                                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g));
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < kMB; ++i)
       dma16(sb, voff[i], __builtin_amdgcn_readfirstlane(lds_wave + (uint32_t)(slot * (kFM * kFK * 2) + 32 * 128 * i)));
   };
   const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
@@ -368,7 +369,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
       static_for<4>([&]<int S>() {
         if constexpr (S < 3) bf[(S + 1) & 1] = TT::template frag<G, S + 1>(raw, sc);
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
+        for (int mb = 0; mb < kMB; ++mb)
           acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(read_a(slot, mb, S), bf[S & 1], acc[mb], 0, 0, 0);
       });
       if constexpr (G == kP - 1) TT::prep(raw, sc, h);
@@ -383,7 +384,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     // raw sums of this K part: tile-local row-major [256][128] f32 block
     float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kFM * kFN) + 4 * h * kFN + 32 * wave + l32;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb)
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kFN] = acc[mb][e];
     return;
@@ -408,8 +409,8 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
       };
       load_full(0, r[0]);
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        if (mb + 1 < 8) load_full(mb + 1, r[(mb + 1) & 1]);
+      for (int mb = 0; mb < kMB; ++mb) {
+        if (mb + 1 < kMB) load_full(mb + 1, r[(mb + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int e = 0; e < 16; ++e)
@@ -427,8 +428,8 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     };
     load_block(0, r[0]);
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      if (mb + 1 < 8) load_block(mb + 1, r[(mb + 1) & 1]);
+    for (int mb = 0; mb < kMB; ++mb) {
+      if (mb + 1 < kMB) load_block(mb + 1, r[(mb + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -443,13 +444,13 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
       // whole tile: no row checks, the activation chosen once
       if (act == MQ_ACT_NONE_) {
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
+        for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
             store_out_stream<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, acc[mb][e] + bv);
       } else {
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
+        for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
           for (int e = 0; e < 16; ++e)
             store_out_stream<OUT>(yc + (mb * 32 + 8 * (e >> 2) + (e & 3)) * ldy, act_out<OUT>(acc[mb][e] + bv, MQ_ACT_GELU_));
@@ -458,7 +459,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     }
     if (!colok) return;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb)
+    for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
@@ -469,7 +470,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
 
 // Tail tiles split over K: y = epi(sum of the kparts raw sums in part order
 // + bias), one thread per 4 columns of a tile row.
-template <typename OUT>
+template <typename OUT, int kFM>
 __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__restrict__ partial, int kparts,
                                                                int full_tiles, int tiles_n, int64_t m, int64_t n,
                                                                OUT *__restrict__ y, int64_t ldy,
@@ -546,13 +547,48 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
     if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
 }
 
-template <typename OUT, bool GATED>
+template <typename OUT, bool GATED, int FM>
 static void launch_fast(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                         int64_t lda, void *y, int64_t ldy, const float *bias, const float *gate, int act,
                         int tiles_m, int tiles_n, int full, int kp, float *partial, int wgs, hipStream_t stream) {
-  hipLaunchKernelGGL((gemm_fast_kernel<MQ_GEMM_TYPE, OUT, GATED>), dim3(wgs), dim3(kFastThreads), 0, stream, w, n,
-                     k, ntiles_w, a, m, lda, static_cast<OUT *>(y), ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
-                     partial);
+  hipLaunchKernelGGL((gemm_fast_kernel<MQ_GEMM_TYPE, OUT, GATED, FM>), dim3(wgs), dim3(kFastThreads), 0, stream, w,
+                     n, k, ntiles_w, a, m, lda, static_cast<OUT *>(y), ldy, bias, gate, act, tiles_m, tiles_n, full,
+                     kp, partial);
+}
+
+// One weight type's fast GEMM with FM-row block tiles (the tail plan's fm).
+template <int FM>
+static void launch_fast_fm(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
+                           int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
+                           int act, const GemmTail &tail, float *partial, hipStream_t stream) {
+  const int tiles_m = (int)((m + FM - 1) / FM);
+  const int tiles_n = (int)((n + kFN - 1) / kFN);
+  const int grid = tiles_m * tiles_n;
+  const bool split = partial && tail.kparts > 1;
+  const int full = split ? tail.full_tiles : grid;
+  const int kp = split ? tail.kparts : 1;
+  const int wgs = full + (grid - full) * kp;
+  if (gate)
+    launch_fast<float, true, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
+                                 partial, wgs, stream);
+  else if (y_type == F32)
+    launch_fast<float, false, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
+                                  kp, partial, wgs, stream);
+  else
+    launch_fast<__bf16, false, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
+                                   kp, partial, wgs, stream);
+  if (split) {
+    const dim3 rgrid(FM * kFN / 4 / 256, (unsigned)(grid - full));
+    const uintptr_t ya = y_type == F32 ? 15 : 7;
+    const int vec = (reinterpret_cast<uintptr_t>(y) & ya) == 0 && ldy % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(bias) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
+    if (y_type == F32)
+      hipLaunchKernelGGL((gemm_tail_reduce_kernel<float, FM>), rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
+                         m, n, static_cast<float *>(y), ldy, bias, gate, act, vec);
+    else
+      hipLaunchKernelGGL((gemm_tail_reduce_kernel<__bf16, FM>), rgrid, dim3(256), 0, stream, partial, kp, full,
+                         tiles_n, m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act, vec);
+  }
 }
 
 template <int T>
@@ -560,34 +596,12 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
                             int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
                             int act, const GemmTail &tail, float *partial, hipStream_t stream) {
   if (gemm_fast_ok(T, m, k, lda)) {
-    const int tiles_m = (int)((m + kFM - 1) / kFM);
-    const int tiles_n = (int)((n + kFN - 1) / kFN);
-    const int grid = tiles_m * tiles_n;
-    const bool split = partial && tail.kparts > 1;
-    const int full = split ? tail.full_tiles : grid;
-    const int kp = split ? tail.kparts : 1;
-    const int wgs = full + (grid - full) * kp;
-    if (gate)
-      launch_fast<float, true>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
-                               partial, wgs, stream);
-    else if (y_type == F32)
-      launch_fast<float, false>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
-                                kp, partial, wgs, stream);
+    if (tail.fm == 64)
+      launch_fast_fm<64>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
+    else if (tail.fm == 128)
+      launch_fast_fm<128>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
     else
-      launch_fast<__bf16, false>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
-                                 kp, partial, wgs, stream);
-    if (split) {
-      const dim3 rgrid(kFM * kFN / 4 / 256, (unsigned)(grid - full));
-      const uintptr_t ya = y_type == F32 ? 15 : 7;
-      const int vec = (reinterpret_cast<uintptr_t>(y) & ya) == 0 && ldy % 4 == 0 &&
-                      (reinterpret_cast<uintptr_t>(bias) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
-      if (y_type == F32)
-        hipLaunchKernelGGL(gemm_tail_reduce_kernel<float>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n, m,
-                           n, static_cast<float *>(y), ldy, bias, gate, act, vec);
-      else
-        hipLaunchKernelGGL(gemm_tail_reduce_kernel<__bf16>, rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
-                           m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act, vec);
-    }
+      launch_fast_fm<256>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
     return hipGetLastError();
   }
   const int tiles_m = (int)((m + kBM - 1) / kBM);
@@ -612,16 +626,52 @@ template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64
 // Tail plan of the fast kernel: when the last round of tiles over the CUs'
 // workgroup slots is partial, split each of those tail tiles into kp K parts
 // so that they fill one round.
-GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus) {
-  const int64_t tiles = ((m + kGemmTileM - 1) / kGemmTileM) * ((n + kGemmTileN - 1) / kGemmTileN);
-  const int64_t slots = (int64_t)cus * kGemmWgsPerCu;
+// K parts of each tail tile for row tiles of fm (1: no split).
+static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, int fm, int64_t *rem_out) {
+  const int64_t tiles = ((m + fm - 1) / fm) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int64_t slots = (int64_t)cus * gemm_wgs_per_cu(fm);
   const int64_t rem = tiles % slots;  // tiles of the last, partial round
   const int64_t units = k / gemm_unit_k(type);
-  GemmTail t{(int)tiles, 1};
-  if (rem == 0 || units < 2) return t;
+  if (rem_out) *rem_out = rem;
+  if (rem == 0 || units < 2) return 1;
   int64_t kp = slots / rem;  // K parts per tail tile: they fill one round
   kp = kp < units ? kp : units;
   kp = kp < kGemmMaxKParts ? kp : kGemmMaxKParts;
+  return kp < 2 ? 1 : kp;
+}
+
+// Rows per block tile.  256-row tiles decode each weight once per 256 rows of
+// x; for small m most of such a tile is padding, so up to 128 rows the tile
+// shrinks to 64 or 128 rows (more tiles, three or four workgroups per CU) and
+// from 129 to 256 rows to 128.  Up to 128 rows the launch is latency-bound:
+// its time follows the K units each workgroup walks after the tail split
+// (measured on the T5 / FLUX / Qwen shapes at m = 77 and 128: 0.71-0.85 of the
+// 256-row time), so the candidate with fewer units per workgroup wins, 64
+// rows on a tie.
+int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus) {
+  if (m > 256) return 256;
+  if (m > 128) return 128;
+  const int64_t units = k / gemm_unit_k(type);
+  int best = 64;
+  int64_t best_depth = -1;
+  for (int fm : {64, 128}) {
+    const int64_t kp = tail_kparts(type, m, n, k, cus, fm, nullptr);
+    const int64_t depth = (units + kp - 1) / kp;
+    if (best_depth < 0 || depth < best_depth) {
+      best = fm;
+      best_depth = depth;
+    }
+  }
+  return best;
+}
+
+GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus, bool split) {
+  const int fm = gemm_tile_m(type, m, n, k, cus);
+  const int64_t tiles = ((m + fm - 1) / fm) * ((n + kGemmTileN - 1) / kGemmTileN);
+  GemmTail t{(int)tiles, 1, fm};
+  if (!split) return t;
+  int64_t rem = 0;
+  const int64_t kp = tail_kparts(type, m, n, k, cus, fm, &rem);
   if (kp < 2) return t;
   t.full_tiles = (int)(tiles - rem);
   t.kparts = (int)kp;
@@ -629,9 +679,9 @@ GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus) {
 }
 
 size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n) {
-  const int64_t tiles = ((m + kGemmTileM - 1) / kGemmTileM) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int64_t tiles = ((m + t.fm - 1) / t.fm) * ((n + kGemmTileN - 1) / kGemmTileN);
   if (t.kparts < 2) return 0;
-  return (size_t)(tiles - t.full_tiles) * t.kparts * kGemmTileM * kGemmTileN * sizeof(float);
+  return (size_t)(tiles - t.full_tiles) * t.kparts * t.fm * kGemmTileN * sizeof(float);
 }
 
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,

@@ -58,15 +58,24 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const voi
 // runs every tile whole.  Other k take a generic 256 x 256 kernel.
 constexpr int kGemmTileM = 256;      // fast kernel block tile (rows of x)
 constexpr int kGemmTileN = 128;      // fast kernel block tile (output features)
-constexpr int kGemmWgsPerCu = 2;     // fast kernel workgroups resident per CU
+constexpr int kGemmWgsPerCu = 2;     // fast kernel workgroups resident per CU (256-row tiles)
+// Workgroups of the fast kernel resident per CU for a row tile of fm: its
+// registers (about 230 / 145 / 110 VGPRs at 256 / 128 / 64 rows) allow 2 / 3
+// / 4 waves per SIMD, and the LDS (32 / 16 / 8 KiB per slot, two slots) holds
+// them.
+inline int gemm_wgs_per_cu(int fm) { return fm == 64 ? 4 : fm == 128 ? 3 : 2; }
 constexpr int kGemmMaxKParts = 8;
 struct GemmTail {
   int full_tiles;  // tiles run whole (all of them when kparts == 1)
   int kparts;      // K parts per tail tile
+  int fm;          // rows per block tile: 256, or 128 / 64 for small m
 };
 // K unit of the fast kernel per weight type (the decoder's unit in mq_bfrag.h).
 inline int gemm_unit_k(int type) { return type == Q8_0 ? 128 : 256; }
-GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus);
+// Rows per block tile of the fast kernel for a call of m rows.
+int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus);
+// The call's tile plan: its fm, and with `split` the K split of a partial last round.
+GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus, bool split);
 size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n);
 // The fast kernel (and tail splitting) applies: whole K units, 16-byte aligned
 // rows, and byte offsets of x that fit the 31-bit buffer range.

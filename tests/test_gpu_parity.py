@@ -348,6 +348,36 @@ def test_gemm_matches_f64_oracle(dev, torch, t, mnk):
     assert np.isfinite(y).all()
 
 
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+@pytest.mark.parametrize("m", [9, 63, 64, 65, 77, 128, 129, 256, 512])
+def test_gemm_row_tiles_64_128_256(dev, torch, t, m):
+    """The fast GEMM's 64-, 128- and 256-row block tiles, chosen by m (64 up to 64 rows,
+    128 up to 128, 256 above), at and around each boundary: rel-L2 to f64, rows past m
+    untouched (the output is a view into a larger buffer), bf16 output, and the gated
+    epilogue; n = 4096 at k = 1024 leaves few tiles, so the partial last round also
+    takes the K split."""
+    n, k = 4096, 1024
+    _say(f"gemm row tiles {t.name} m={m}")
+    blocks = _weights(int(t), n, k, seed=3 * m + 1)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = np.random.default_rng(m + 7).standard_normal((m, k)).astype(np.float32)
+    xt = torch.from_numpy(x).cuda()
+    ref = O.matmul_f64(int(t), x, blocks, n, k)
+    buf = torch.full((m + 5, n), 7.0, device="cuda")
+    y = QMatMul(qt).forward(xt, out=buf[:m])
+    torch.cuda.synchronize()
+    assert O.rel_l2(y.cpu().numpy(), ref) <= GEMM_TOL
+    assert torch.all(buf[m:] == 7.0)
+    yb = QMatMul(qt).forward(xt.to(torch.bfloat16), out_dtype=torch.bfloat16).float().cpu().numpy()
+    refb = O.matmul_f64(int(t), xt.to(torch.bfloat16).float().cpu().numpy(), blocks, n, k)
+    assert O.rel_l2(yb, refb) <= GEMM_TOL
+    res = torch.from_numpy(np.random.default_rng(m).standard_normal((m, n)).astype(np.float32)).cuda()
+    gate = torch.from_numpy(np.random.default_rng(m + 1).standard_normal(n).astype(np.float32)).cuda()
+    want = res.double().cpu().numpy() + gate.double().cpu().numpy() * ref
+    mold_amd.Linear(qt).gated_add(xt, gate, res)
+    assert O.rel_l2(res.cpu().numpy(), want) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("t", [GgmlDType.Q4_0, GgmlDType.Q8_0, GgmlDType.Q5_1], ids=lambda t: t.name)
 def test_gemm_k_not_multiple_of_64(dev, torch, t):
     # 32-element blocks allow k = 32 * odd: the last K step is half padding
