@@ -388,6 +388,22 @@ def bench_encoder_decode(dev, args):
                         "frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
             log(f"  T5 {tname} {label} m={m}: {ms*1e3:.1f} us {enc[-1]['tflops']} TFLOP/s")
             del mm
+    # small-m linears: T5 at a 77-token prompt, Qwen-Image's text stream (256 tokens)
+    mid = []
+    for label, tname, n, k in (("t5 attn_q", "Q8_0", 4096, 4096), ("t5 ffn_up", "Q8_0", 10240, 4096),
+                               ("t5 ffn_down", "Q8_0", 4096, 10240), ("qwen txt add_qkv", "Q3_K", 9216, 3072),
+                               ("qwen txt to_add_out", "Q4_K", 3072, 3072)):
+        mm = mold_amd.QMatMul(make_weight(dev, GgmlDType[tname], n, k, seed=72))
+        for m_ in (77, 256):
+            x = torch.randn((m_, k), device="cuda", generator=g)
+            y = torch.empty((m_, n), device="cuda")
+            _, ms = timed(lambda: mm.forward(x, out=y), max(50, args.steps), 5, prewarm_s=0.05)
+            fl = 2.0 * m_ * n * k
+            mid.append({"weight": tname, "linear": label, "m": m_, "n": n, "k": k, "us": round(ms * 1e3, 2),
+                        "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                        "frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)})
+            log(f"  {label} {tname} m={m_}: {ms*1e3:.1f} us {mid[-1]['tflops']} TFLOP/s")
+        del mm
     dec = []
     for tname in ("Q8_0", "Q6_K", "Q5_K", "Q4_K", "Q4_0"):
         for n, k in ((4096, 4096), (10240, 4096), (4096, 10240)):
@@ -420,8 +436,9 @@ def bench_encoder_decode(dev, args):
             log(f"  decode {tname} {k}->{n}: {ms*1e3:.2f} us {dec[-1]['gbs']} GB/s")
             del graph, mms, first
             torch.cuda.empty_cache()
-    return {"t5_encoder_m512": enc, "decode_gemv_m1": dec,
-            "what": "T5-XXL encoder linears (f32 x staged to bf16 + fused GEMM) and LLM-decode M=1 GEMVs "
+    return {"t5_encoder_m512": enc, "small_m_gemm": mid, "decode_gemv_m1": dec,
+            "what": "T5-XXL encoder linears (f32 x staged to bf16 + fused GEMM) at M=512; small-m GEMMs "
+                    "(64- / 128-row tiles) at M=77 and 256; LLM-decode M=1 GEMVs "
                     "(f32 x; Q4_K takes the Q8_K integer-dot GEMV, other types the f32-FMA GEMV)"}
 
 

@@ -566,10 +566,15 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
     for (int m = 0; m < M; ++m) red[slot * M + m] = acc[m];
   };
 
-  // 1. the first item's weights, then x into LDS by direct loads (item j =
-  //    row m's elements 256 c .. +255: one 1 KiB wave load), one wait for both
+  // 1. x into LDS by direct loads (item j = row m's elements 256 c .. +255:
+  //    one 1 KiB wave load) and the first item's weights.  For the k-quants x
+  //    goes first and the weights once it has landed (as in the Q4_K kernel: x
+  //    then does not queue behind the weight stream; Q5_K / Q6_K 3-7 % faster
+  //    at m = 1 on the decode shapes); for the 32-element types the weights go
+  //    first and one wait covers both (x first measured -2 .. +3 % there).
+  constexpr bool kXFirst = TYPE == Q2_K || TYPE == Q3_K || TYPE == Q5_K || TYPE == Q6_K;
   typename TT::Raw a, b;
-  load_item(tid, a);
+  if (!kXFirst) load_item(tid, a);
   {
     const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t *)smem;
     const int items = (int)(M * (k >> 8));
@@ -582,6 +587,7 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if (kXFirst) load_item(tid, a);
 
   // 2. items, the next one's loads in flight while the current one computes
   for (int p = tid;; p += 2 * kFragThreads) {
