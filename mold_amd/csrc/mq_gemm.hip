@@ -3,19 +3,23 @@
 //
 // gemm_fast_kernel (k a whole number of the weight type's K units) is the
 // path every BASELINE shape takes.  It is shaped for gfx950's CUs (4 SIMDs,
-// 512 VGPRs per SIMD lane, 160 KiB LDS) so that TWO workgroups share each CU:
-//   * workgroup = 4 waves (one per SIMD), block tile 256 (m) x 128 (n); with
-//     two workgroups per CU every SIMD holds two waves, so one wave's MFMAs
-//     run while the other decodes weights, and one workgroup's epilogue,
-//     prologue and memory waits overlap the other's main loop;
-//   * wave w owns output features 32w .. 32w+31 of the tile for all 256
+// 512 VGPRs per SIMD lane, 160 KiB LDS) so that every SIMD holds two waves
+// (one wave's MFMAs run while the other decodes weights):
+//   * large m: workgroup = 8 waves (two per SIMD), block tile 256 (m) x 256
+//     (n), one workgroup per CU, so the 256 x 64 activation tile of a K step
+//     is fetched once for 256 output features (against two 4-wave 256 x 128
+//     workgroups per CU: 3-8 % faster on every large BASELINE shape, same
+//     outputs); small m: 64- or 128-row tiles of 4 waves x 128 features, three
+//     or four workgroups per CU;
+//   * wave w owns output features 32w .. 32w+31 of the tile for all its
 //     rows: lane (l32, h) decodes weight row l32 of that run straight into
 //     the MFMA B operand (per-type decoders, mq_bfrag.h), so every weight is
 //     decoded once per block tile and B never touches LDS;
-//   * v_mfma_f32_32x32x16_bf16, 8 accumulator tiles (128 f32) per lane;
-//   * the bf16 activation tile (256 x 64 per K step) goes global -> LDS one
+//   * v_mfma_f32_32x32x16_bf16, 8 accumulator tiles (128 f32) per lane at 256
+//     rows;
+//   * the bf16 activation tile (rows x 64 per K step) goes global -> LDS one
 //     step ahead by LDS DMA (global_load_lds_dwordx4: no VGPRs, no LDS
-//     write instructions) through a 2-slot ring (2 x 32 KiB per workgroup);
+//     write instructions) through a 2-slot ring (2 x 32 KiB at 256 rows);
 //     the step's weight loads are issued with it at the step's start and
 //     both are awaited once, at the step barrier;
 //   * rows are 128 B, chunk c of row r in slot c ^ ((r >> 1) & 7), so the
@@ -218,9 +222,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Fast path.  Block tile kFM x kFN, K step kFK; see the file comment.
-constexpr int kFN = kGemmTileN, kFK = 64;
-constexpr int kFastThreads = 256;
+// Fast path.  Block tile kFM x (32 kW), K step kFK; see the file comment.
+constexpr int kFK = 64;
 constexpr int MQ_ACT_NONE_ = 0;  // mq_act MQ_ACT_NONE
 constexpr int MQ_ACT_GELU_ = 1;  // mq_act MQ_ACT_GELU_TANH (the only other value)
 
@@ -257,14 +260,16 @@ __device__ __forceinline__ void step_barrier() {
   asm volatile("s_barrier" ::: "memory");
 }
 
-template <int TYPE, typename OUT, bool GATED, int kFM>
-__global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
+template <int TYPE, typename OUT, bool GATED, int kFM, int kW>
+__global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
     WView w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *__restrict__ a, int64_t m, int64_t lda,
     OUT *y, int64_t ldy, const float *__restrict__ bias, const float *__restrict__ gate, int act, int tiles_m,
     int tiles_n, int full_tiles, int kparts, float *__restrict__ partial) {
   using TT = bfrag::T<TYPE>;
   constexpr int kP = TT::kUnitK / kFK;  // K steps per weight unit
   constexpr int kMB = kFM / 32;         // 32-row MFMA blocks of the tile
+  constexpr int kFNW = 32 * kW;         // output features of the tile
+  constexpr int kDM = kFM / (8 * kW);   // A DMA loads per wave and step
   __shared__ uint4 lds_a[2][kFM * kFK / 8];
 
   // Workgroups 0 .. full_tiles-1 run whole tiles (XCD-aware order over
@@ -289,7 +294,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
   const int64_t m0 = (int64_t)mt * kFM;
-  const int64_t c0 = (int64_t)nt * kFN + 32 * wave;  // this wave's first output feature
+  const int64_t c0 = (int64_t)nt * kFNW + 32 * wave;  // this wave's first output feature
   const int64_t wt_raw = c0 / kRowTile;              // its weight tile
   const int wrow = (int)(c0 - wt_raw * kRowTile) + l32;  // this lane's row in that tile
   const int64_t wt = wt_raw < ntiles_w ? wt_raw : ntiles_w - 1;  // keep reads in bounds
@@ -313,10 +318,10 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   // uniform base address.
   const int ac = tid & 7, ar = tid >> 3;
   const int gch = ac ^ ((ar >> 1) & 7);
-  uint32_t voff[kMB];
+  uint32_t voff[kDM];
 #pragma unroll
-  for (int i = 0; i < kMB; ++i) {
-    const int64_t r = m0 + ar + 32 * i < m ? m0 + ar + 32 * i : m - 1;
+  for (int i = 0; i < kDM; ++i) {
+    const int64_t r = m0 + ar + 8 * kW * i < m ? m0 + ar + 8 * kW * i : m - 1;
     voff[i] = (uint32_t)((r * lda + gch * 8) * 2);
   }
   const uint32_t akb = (uint32_t)(ub * TT::kUnitK * 2);
@@ -326,8 +331,9 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
     const char *sb = reinterpret_cast<const char *>(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32)) << 32) |
                                                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g));
 #pragma unroll
-    for (int i = 0; i < kMB; ++i)
-      dma16(sb, voff[i], __builtin_amdgcn_readfirstlane(lds_wave + (uint32_t)(slot * (kFM * kFK * 2) + 32 * 128 * i)));
+    for (int i = 0; i < kDM; ++i)
+      dma16(sb, voff[i],
+            __builtin_amdgcn_readfirstlane(lds_wave + (uint32_t)(slot * (kFM * kFK * 2) + 8 * kW * 128 * i)));
   };
   const int swz = (l32 >> 1) & 7;  // LDS swizzle key of every row this lane reads
   auto read_a = [&](int slot, int mb, int S) -> bf16x8 {
@@ -382,11 +388,11 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
   if (c0 >= n) return;
   if (part >= 0) {
     // raw sums of this K part: tile-local row-major [256][128] f32 block
-    float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kFM * kFN) + 4 * h * kFN + 32 * wave + l32;
+    float *pt = partial + ((int64_t)(v - full_tiles) * kparts + part) * (kFM * kFNW) + 4 * h * kFNW + 32 * wave + l32;
 #pragma unroll
     for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kFN] = acc[mb][e];
+      for (int e = 0; e < 16; ++e) pt[(mb * 32 + 8 * (e >> 2) + (e & 3)) * kFNW] = acc[mb][e];
     return;
   }
   const int64_t col = c0 + l32;
@@ -470,7 +476,7 @@ __global__ __launch_bounds__(kFastThreads, 2) void gemm_fast_kernel(
 
 // Tail tiles split over K: y = epi(sum of the kparts raw sums in part order
 // + bias), one thread per 4 columns of a tile row.
-template <typename OUT, int kFM>
+template <typename OUT, int kFM, int kFN>
 __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__restrict__ partial, int kparts,
                                                                int full_tiles, int tiles_n, int64_t m, int64_t n,
                                                                OUT *__restrict__ y, int64_t ldy,
@@ -547,46 +553,48 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
     if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
 }
 
-template <typename OUT, bool GATED, int FM>
+template <typename OUT, bool GATED, int FM, int W>
 static void launch_fast(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                         int64_t lda, void *y, int64_t ldy, const float *bias, const float *gate, int act,
                         int tiles_m, int tiles_n, int full, int kp, float *partial, int wgs, hipStream_t stream) {
-  hipLaunchKernelGGL((gemm_fast_kernel<MQ_GEMM_TYPE, OUT, GATED, FM>), dim3(wgs), dim3(kFastThreads), 0, stream, w,
+  hipLaunchKernelGGL((gemm_fast_kernel<MQ_GEMM_TYPE, OUT, GATED, FM, W>), dim3(wgs), dim3(64 * W), 0, stream, w,
                      n, k, ntiles_w, a, m, lda, static_cast<OUT *>(y), ldy, bias, gate, act, tiles_m, tiles_n, full,
                      kp, partial);
 }
 
-// One weight type's fast GEMM with FM-row block tiles (the tail plan's fm).
-template <int FM>
+// One weight type's fast GEMM with FM-row block tiles of W waves (W * 32
+// output features), and the reduce of its split tail tiles.
+template <int FM, int W>
 static void launch_fast_fm(const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a, int64_t m,
                            int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
                            int act, const GemmTail &tail, float *partial, hipStream_t stream) {
+  constexpr int FN = 32 * W;
   const int tiles_m = (int)((m + FM - 1) / FM);
-  const int tiles_n = (int)((n + kFN - 1) / kFN);
+  const int tiles_n = (int)((n + FN - 1) / FN);
   const int grid = tiles_m * tiles_n;
   const bool split = partial && tail.kparts > 1;
   const int full = split ? tail.full_tiles : grid;
   const int kp = split ? tail.kparts : 1;
   const int wgs = full + (grid - full) * kp;
   if (gate)
-    launch_fast<float, true, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, gate, act, tiles_m, tiles_n, full, kp,
-                                 partial, wgs, stream);
+    launch_fast<float, true, FM, W>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, gate, act, tiles_m, tiles_n, full,
+                                    kp, partial, wgs, stream);
   else if (y_type == F32)
-    launch_fast<float, false, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
-                                  kp, partial, wgs, stream);
+    launch_fast<float, false, FM, W>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n,
+                                     full, kp, partial, wgs, stream);
   else
-    launch_fast<__bf16, false, FM>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n, full,
-                                   kp, partial, wgs, stream);
+    launch_fast<__bf16, false, FM, W>(w, n, k, ntiles_w, a, m, lda, y, ldy, bias, nullptr, act, tiles_m, tiles_n,
+                                      full, kp, partial, wgs, stream);
   if (split) {
-    const dim3 rgrid(FM * kFN / 4 / 256, (unsigned)(grid - full));
+    const dim3 rgrid(FM * FN / 4 / 256, (unsigned)(grid - full));
     const uintptr_t ya = y_type == F32 ? 15 : 7;
     const int vec = (reinterpret_cast<uintptr_t>(y) & ya) == 0 && ldy % 4 == 0 &&
                     (reinterpret_cast<uintptr_t>(bias) & 15) == 0 && (reinterpret_cast<uintptr_t>(gate) & 15) == 0;
     if (y_type == F32)
-      hipLaunchKernelGGL((gemm_tail_reduce_kernel<float, FM>), rgrid, dim3(256), 0, stream, partial, kp, full, tiles_n,
-                         m, n, static_cast<float *>(y), ldy, bias, gate, act, vec);
+      hipLaunchKernelGGL((gemm_tail_reduce_kernel<float, FM, FN>), rgrid, dim3(256), 0, stream, partial, kp, full,
+                         tiles_n, m, n, static_cast<float *>(y), ldy, bias, gate, act, vec);
     else
-      hipLaunchKernelGGL((gemm_tail_reduce_kernel<__bf16, FM>), rgrid, dim3(256), 0, stream, partial, kp, full,
+      hipLaunchKernelGGL((gemm_tail_reduce_kernel<__bf16, FM, FN>), rgrid, dim3(256), 0, stream, partial, kp, full,
                          tiles_n, m, n, static_cast<__bf16 *>(y), ldy, bias, gate, act, vec);
   }
 }
@@ -597,11 +605,11 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
                             int act, const GemmTail &tail, float *partial, hipStream_t stream) {
   if (gemm_fast_ok(T, m, k, lda)) {
     if (tail.fm == 64)
-      launch_fast_fm<64>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
+      launch_fast_fm<64, 4>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
     else if (tail.fm == 128)
-      launch_fast_fm<128>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
+      launch_fast_fm<128, 4>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
     else
-      launch_fast_fm<256>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
+      launch_fast_fm<256, 8>(w, n, k, ntiles_w, a, m, lda, y, y_type, ldy, bias, gate, act, tail, partial, stream);
     return hipGetLastError();
   }
   const int tiles_m = (int)((m + kBM - 1) / kBM);
@@ -628,7 +636,8 @@ template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64
 // so that they fill one round.
 // K parts of each tail tile for row tiles of fm (1: no split).
 static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, int fm, int64_t *rem_out) {
-  const int64_t tiles = ((m + fm - 1) / fm) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int fn = gemm_tile_n(fm);
+  const int64_t tiles = ((m + fm - 1) / fm) * ((n + fn - 1) / fn);
   const int64_t slots = (int64_t)cus * gemm_wgs_per_cu(fm);
   const int64_t rem = tiles % slots;  // tiles of the last, partial round
   const int64_t units = k / gemm_unit_k(type);
@@ -667,7 +676,8 @@ int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus) {
 
 GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus, bool split) {
   const int fm = gemm_tile_m(type, m, n, k, cus);
-  const int64_t tiles = ((m + fm - 1) / fm) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int fn = gemm_tile_n(fm);
+  const int64_t tiles = ((m + fm - 1) / fm) * ((n + fn - 1) / fn);
   GemmTail t{(int)tiles, 1, fm};
   if (!split) return t;
   int64_t rem = 0;
@@ -679,9 +689,10 @@ GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus, bool
 }
 
 size_t gemm_tail_bytes(const GemmTail &t, int64_t m, int64_t n) {
-  const int64_t tiles = ((m + t.fm - 1) / t.fm) * ((n + kGemmTileN - 1) / kGemmTileN);
+  const int fn = gemm_tile_n(t.fm);
+  const int64_t tiles = ((m + t.fm - 1) / t.fm) * ((n + fn - 1) / fn);
   if (t.kparts < 2) return 0;
-  return (size_t)(tiles - t.full_tiles) * t.kparts * t.fm * kGemmTileN * sizeof(float);
+  return (size_t)(tiles - t.full_tiles) * t.kparts * t.fm * fn * sizeof(float);
 }
 
 hipError_t launch_gemm(int type, const WView &w, int64_t n, int64_t k, int64_t ntiles_w, const __bf16 *a,

@@ -56,14 +56,15 @@ hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const voi
 // (gemm_tail_bytes of it), added in part order by a second kernel that
 // applies the epilogue: the plan comes from gemm_tail_plan; partial == NULL
 // runs every tile whole.  Other k take a generic 256 x 256 kernel.
-constexpr int kGemmTileM = 256;      // fast kernel block tile (rows of x)
-constexpr int kGemmTileN = 128;      // fast kernel block tile (output features)
-constexpr int kGemmWgsPerCu = 2;     // fast kernel workgroups resident per CU (256-row tiles)
+constexpr int kGemmTileM = 256;      // fast kernel block tile (rows of x) for large m
+// Output features of a block tile: 32 per wave; 256-row tiles run 8 waves
+// (256 x 256, one workgroup per CU), 128- and 64-row tiles 4 (x 128).
+inline int gemm_tile_n(int fm) { return fm == 256 ? 256 : 128; }
 // Workgroups of the fast kernel resident per CU for a row tile of fm: its
-// registers (about 230 / 145 / 110 VGPRs at 256 / 128 / 64 rows) allow 2 / 3
+// registers (about 225 / 145 / 110 VGPRs at 256 / 128 / 64 rows) allow 2 / 3
 // / 4 waves per SIMD, and the LDS (32 / 16 / 8 KiB per slot, two slots) holds
-// them.
-inline int gemm_wgs_per_cu(int fm) { return fm == 64 ? 4 : fm == 128 ? 3 : 2; }
+// them: one 8-wave workgroup, or 3 / 4 of 4 waves.
+inline int gemm_wgs_per_cu(int fm) { return fm == 64 ? 4 : fm == 128 ? 3 : 1; }
 constexpr int kGemmMaxKParts = 8;
 struct GemmTail {
   int full_tiles;  // tiles run whole (all of them when kparts == 1)
