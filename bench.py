@@ -34,7 +34,8 @@ Also on the same JSON line:
     so reads miss the Infinity Cache, in GB/s of algorithmic bytes against
     the 8 TB/s HBM peak.  The rotation is captured once in a HIP graph and
     replayed, so the figure is the kernels' own rate, not Python's launch
-    rate;
+    rate.  Beside it, "read_ceiling": a single streaming-read launch of the
+    same weight bytes (libmoldq_probe.so), cold, in the same run;
   * "dense_bf16_ceiling": torch's bf16 linear (hipBLASLt) at the headline shape
     with a dense bf16 weight, the achievable-MFMA reference;
   * "encoder_decode": T5-XXL encoder linears at M=512 and LLM-decode M=1
@@ -62,10 +63,10 @@ Also on the same JSON line:
     prompt) in ms ("cfg_batch2_ms"), and its 121 modulation linears' stacked
     GEMV (2,217,984 x 3072 Q4_K) at M = 1 and 2 ("modulation_stack");
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
-    integer block dots, threads over output columns), restated in C under
-    oracle/, timed on a bounded row sample of the headline workload on this
-    host's cores for the portable build and for a -march=native build
-    compiled on this host (the faster is `value`), with the CPU model named.
+    integer block dots, threads over output columns), restated as scalar C
+    under oracle/ (gcc -O3, portable x86-64-v2 build), timed on a bounded row
+    sample of the headline workload on the host cores this process may use
+    (`nproc`, up to the 16-core share of one GPU), with the CPU model named.
 
 Weights are N(0, 0.02^2) quantized to GGUF blocks on the GPU by libmoldq's
 quantizer; activations are N(0, 1) from torch's seeded generator.
@@ -489,16 +490,54 @@ def bench_lora(dev, args):
     return res
 
 
+def read_ceiling(nbytes, copies, args):
+    """A single-launch streaming read of `nbytes` (libmoldq_probe.so: one
+    512-thread workgroup per CU over a contiguous share, nontemporal 16-byte
+    loads, as the GEMV lays out its weight stream), cold: `copies` distinct
+    buffers (> 256 MB together, past the Infinity Cache) replayed from a HIP
+    graph.  The ceiling a single GEMV launch of the same weight bytes can reach."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "mold_amd", "libmoldq_probe.so"))
+    lib.mqp_stream_read.restype = ctypes.c_int
+    lib.mqp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    wgs = torch.cuda.get_device_properties(0).multi_processor_count
+    bufs = torch.randint(0, 255, (copies, nbytes), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(wgs, dtype=torch.int32, device="cuda")
+    cap = torch.cuda.Stream()
+
+    def run():
+        for i in range(copies):
+            rc = lib.mqp_stream_read(bufs[i].data_ptr(), nbytes, sink.data_ptr(), wgs, cap.cuda_stream)
+            assert rc == 0, rc
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        run()
+    graph.replay()
+    torch.cuda.synchronize()
+    _, ms = timed(graph.replay, max(10, args.steps), 2, prewarm_s=0.1)
+    ms /= copies
+    del graph, bufs
+    return {"bytes": nbytes, "us": round(ms * 1e3, 3), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+
 def bench_gemv(dev, args):
     import torch
     import mold_amd
     from mold_amd import GgmlDType
-    out = []
+    out, ceilings = [], []
     k = 3072
     for n, copies in ((18432, 12), (9216, 20)):
         log(f"GEMV Q4_K 3072->{n}: quantizing {copies} weight copies")
         qts = [make_weight(dev, GgmlDType.Q4_K, n, k, seed=200 + i) for i in range(copies)]
         wbytes = qts[0].storage_size_in_bytes()
+        ceil = read_ceiling(wbytes, copies, args)
+        ceil["n"] = n
+        ceilings.append(ceil)
+        log(f"  streaming-read ceiling of {wbytes} B: {ceil['us']:.2f} us {ceil['gbs']:.0f} GB/s "
+            f"({ceil['frac']:.3f} of peak)")
         mms = [mold_amd.QMatMul(q) for q in qts]
         for m in (1, 2, 4):
             g = torch.Generator(device="cuda").manual_seed(m)
@@ -521,12 +560,16 @@ def bench_gemv(dev, args):
             nbytes = wbytes + 4 * m * k + 4 * m * n
             out.append({"m": m, "n": n, "k": k, "us": round(ms * 1e3, 3), "bytes": nbytes,
                         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)})
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "of_read_ceiling": round(ceil["us"] / (ms * 1e3), 4)})
             log(f"  m={m} n={n}: {ms*1e3:.2f} us  {out[-1]['gbs']:.0f} GB/s")
             del graph
         del mms, qts
         torch.cuda.empty_cache()
-    return out
+    return {"launches": out, "read_ceiling": ceilings,
+            "what": "single Q4_K GEMV launches (f32 x, f32 y) replayed from a HIP graph over distinct weight "
+                    "copies (> 256 MB, so reads come from HBM); read_ceiling: one streaming-read launch of the "
+                    "same weight bytes in the same run; of_read_ceiling = ceiling time / GEMV time"}
 
 
 def bench_stack(stack, ms_list, args):
@@ -673,7 +716,7 @@ def cpu_qwen_baseline(params, inp):
     import torch
     from mold_amd import qwen_image as Q
     from mold_amd.flux import attention_f32
-    threads = min(16, os.cpu_count() or 1)
+    threads, _ = host_threads()
     torch.set_num_threads(threads)
     cfg = params.cfg
     names = [nm for nm in params.lin if not nm.startswith("transformer_blocks.")
@@ -732,7 +775,7 @@ def cpu_flux_baseline(params, inp):
     layer timed on the CPU, extrapolated to 19 + 38 blocks."""
     import torch
     from mold_amd import flux as F
-    threads = min(16, os.cpu_count() or 1)
+    threads, _ = host_threads()
     torch.set_num_threads(threads)
     cfg = params.cfg
     names = [nm for nm in params.lin if not nm.startswith(("double_blocks.", "single_blocks."))
@@ -813,39 +856,42 @@ def pmc_pass(dev, args):
     log("GEMV launches done")
 
 
+def host_threads():
+    """(threads, nproc): the host cores this process may run on (sched_getaffinity,
+    what `nproc` prints), used up to 16, the CPU share of one GPU on these boxes."""
+    nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return min(16, nproc), nproc
+
+
 def cpu_baseline(blocks, x, n, k, budget_s=8.0):
-    """candle CPU QMatMul algorithm (oracle restatement) on a row sample, timed for
-    both builds (portable -march=x86-64-v2, and -march=native compiled on this
-    host); `value` is the faster."""
+    """candle CPU QMatMul algorithm (the oracle's scalar C restatement, portable
+    gcc -O3 -march=x86-64-v2 build) on a row sample of the headline workload.
+    It is candle's algorithm, not candle's SIMD code, so it understates candle's
+    own CPU path; it is a reported baseline only."""
     import numpy as np
     from oracle import oracle as O
-    threads = min(16, os.cpu_count() or 1)
-    builds = [("gcc -O3 -march=x86-64-v2", False)]
-    try:
-        O.native_lib()
-        builds.append(("gcc -O3 -march=native", True))
-    except Exception as err:  # no compiler on this host
-        log(f"native oracle build failed ({err}); timing the portable build only")
+    threads, nproc = host_threads()
+    builds = ["gcc -O3 -march=x86-64-v2"]
     timings = {}
-    for label, native in builds:
+    for label in builds:
         xs = np.ascontiguousarray(x[:8].float().cpu().numpy())
         t0 = time.perf_counter()
-        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads, native=native)
+        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads)
         per_row = (time.perf_counter() - t0) / 8
         rows = int(max(8, min(4608, budget_s / max(per_row, 1e-6))))
         xs = np.ascontiguousarray(x[:rows].float().cpu().numpy())
         t0 = time.perf_counter()
-        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads, native=native)
+        O.matmul_candle(O.Q4_K, xs, blocks, n, k, nthreads=threads)
         dt = time.perf_counter() - t0
         timings[label] = (2.0 * rows * n * k / dt / 1e12, rows, dt)
         log(f"  CPU {label}: {timings[label][0]:.4f} TFLOP/s over {rows} rows ({dt:.1f} s)")
     best = max(timings, key=lambda lb: timings[lb][0])
     tf, rows, dt = timings[best]
-    return {"value": tf, "unit": "TFLOP/s", "cores": threads, "kind": "port", "cpu_model": cpu_model(),
-            "build": best, "all_builds": {lb: round(v[0], 4) for lb, v in timings.items()},
+    return {"value": tf, "unit": "TFLOP/s", "cores": threads, "nproc": nproc, "kind": "port",
+            "cpu_model": cpu_model(), "build": best,
             "sample": f"{rows} of 4608 rows of x [4608,3072] against the full Q4_K W[21504,3072] "
-                      f"({dt:.1f} s; candle CPU algorithm restated in C: x->Q8_K, integer block dots, "
-                      f"{threads} threads over output columns)"}
+                      f"({dt:.1f} s; candle's CPU algorithm restated as scalar C, not candle's SIMD code: "
+                      f"x->Q8_K, integer block dots, {threads} threads over output columns; nproc {nproc})"}
 
 
 def main():

@@ -1,0 +1,48 @@
+// mq_probe.hip — a measurement probe, not part of the library's ABI: the
+// streaming-read ceiling that bench.py sets beside the skinny GEMV.  One
+// launch reads a device buffer once with one 512-thread workgroup per CU and
+// nontemporal 16-byte loads, as the Q4_K GEMV streams its weights, and folds
+// the words into one value per thread so that no load can be dropped.  Built
+// into libmoldq_probe.so, which only bench.py loads.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The bytes are read as 8 KiB blocks, block j * wgs + w by workgroup w, so
+// that at every moment the chip streams one contiguous region (spread over all
+// HBM channels); every load of a round (up to 16 per thread, a thread's whole
+// share at the GEMV shapes) is issued before any of its data is used.
+__global__ __launch_bounds__(512) void stream_read_kernel(const u32x4 *__restrict__ src, int64_t n16,
+                                                         uint32_t *__restrict__ sink) {
+  constexpr int kBatch = 16;
+  const int64_t nblk = (n16 + 511) / 512;
+  uint32_t acc = 0;
+  for (int64_t j0 = 0; j0 * gridDim.x < nblk; j0 += kBatch) {
+    u32x4 v[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      const int64_t i = ((j0 + j) * gridDim.x + blockIdx.x) * 512 + threadIdx.x;
+      v[j] = i < n16 ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  // a store that depends on every word read keeps the loads; it almost never
+  // happens, so the probe writes (nearly) nothing
+  if (acc == 0x9E3779B9u) sink[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+// Reads `bytes` (a multiple of 16, 16-byte aligned) at `src` once on
+// `stream`, `wgs` workgroups; sink holds `wgs` words.  Returns a hipError_t.
+extern "C" int mqp_stream_read(const void *src, size_t bytes, uint32_t *sink, int wgs, void *stream) {
+  if (!src || !sink || wgs <= 0 || (bytes & 15) || (reinterpret_cast<uintptr_t>(src) & 15)) return (int)hipErrorInvalidValue;
+  const int64_t n16 = (int64_t)(bytes / 16);
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)wgs), dim3(512), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const u32x4 *>(src), n16, sink);
+  return (int)hipGetLastError();
+}

@@ -55,22 +55,6 @@ def build() -> str:
     return _LIB_PATH
 
 
-_NATIVE_PATH = os.path.join(_HERE, "liboracle_native.so")
-_native = None
-
-
-def native_lib() -> ctypes.CDLL:
-    """The same oracle compiled on this host with -march=native (the CPU
-    baseline's build: the portable liboracle.so targets x86-64-v2 so that it
-    runs on any box).  Rebuilt on first use in each process, with the
-    committed Makefile, so it always matches the CPU it runs on."""
-    global _native
-    if _native is None:
-        subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle_native.so"], check=True)
-        _native = _bind(ctypes.CDLL(_NATIVE_PATH))
-    return _native
-
-
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
@@ -173,17 +157,14 @@ def vec_dot(t: int, k: int, w_row: np.ndarray, act_row: np.ndarray) -> float:
     return float(lib().orc_vec_dot(t, k, _ptr(w_row), _ptr(act_row)))
 
 
-def matmul_candle(t: int, x: np.ndarray, w_blocks: np.ndarray, n: int, k: int, nthreads: int = 0,
-                  native: bool = False) -> np.ndarray:
-    """candle CPU QMatMul: quantized activations x integer block dots
-    (`native`: the -march=native build of the same code)."""
+def matmul_candle(t: int, x: np.ndarray, w_blocks: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
+    """candle CPU QMatMul: quantized activations x integer block dots."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     m = x.shape[0]
     assert x.shape == (m, k)
     w_blocks = np.ascontiguousarray(w_blocks, dtype=np.uint8)
     y = np.empty((m, n), dtype=np.float32)
-    L = native_lib() if native else lib()
-    rc = L.orc_matmul_candle(t, m, n, k, _ptr(x), _ptr(w_blocks), _ptr(y), nthreads)
+    rc = lib().orc_matmul_candle(t, m, n, k, _ptr(x), _ptr(w_blocks), _ptr(y), nthreads)
     if rc != 0:
         raise ValueError(f"matmul_candle failed rc={rc}")
     return y
