@@ -42,9 +42,11 @@ Also on the same JSON line:
     GEMVs at K=4096 / N=10240 (the text-encoder and prompt-expansion shapes);
   * "lora_merge": device LoRA merge (dequantize -> rank-32 patches ->
     re-quantize) of a single-block linear1, with the host chain on a sample;
-  * "upload": GGUF file -> HBM rate of mq_gguf_load_tensor (pinned,
-    double-buffered) over a 300 MB file just written (so read from the page
-    cache: PCIe and the pipeline, not the disk), and of the host-buffer upload;
+  * "upload": GGUF file -> HBM rate of mq_gguf_load_tensor per tensor and of
+    one batched mq_gguf_load_tensors call (threaded pinned pipeline) over a
+    300 MB file just written (so read from the page cache: PCIe and the
+    pipeline, not the disk), of the host-buffer upload, and the pinned
+    host -> device copy rate of the same process;
   * "flux_step": one FLUX.1-dev-shaped denoising-step forward at 1024^2
     (19 double + 38 single blocks, hidden 3072,
     4096 image + 512 text tokens, every linear Q4_K except the bf16 img_in),
@@ -317,8 +319,10 @@ def bench_dense_ceiling(args):
 
 
 def bench_upload(dev, args):
-    """GGUF file -> HBM and host buffer -> HBM upload rates."""
+    """GGUF file -> HBM and host buffer -> HBM upload rates, beside the pinned
+    host -> device copy rate of the same process (the PCIe ceiling)."""
     import numpy as np
+    import torch
     import mold_amd
     from mold_amd import GgmlDType, gguf
     n, k, count = 21504, 3072, 8
@@ -326,17 +330,34 @@ def bench_upload(dev, args):
     nbytes = n * (k // 256) * 144
     rng = np.random.default_rng(60)
     raw = [rng.integers(0, 256, nbytes, dtype=np.uint8) for _ in range(count)]
+    names = [f"blk.{i}.weight" for i in range(count)]
+    pin = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    pin.copy_(torch.from_numpy(raw[0]))
+    dst = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    for _ in range(3):
+        dst.copy_(pin, non_blocking=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(count):
+        dst.copy_(pin, non_blocking=True)
+    torch.cuda.synchronize()
+    pinned_gbs = count * nbytes / (time.perf_counter() - t0) / 1e9
+    del pin, dst
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "w.gguf")
-        gguf.write(path, [(f"blk.{i}.weight", t, (n, k), r) for i, r in enumerate(raw)])
+        gguf.write(path, [(nm, t, (n, k), r) for nm, r in zip(names, raw)])
         log(f"upload: GGUF file {count * nbytes / 1e6:.0f} MB")
         c = gguf.Content.read(path)
-        c.tensor("blk.0.weight", dev).free()             # first-use setup (pinned buffers, stream)
+        c.tensor(names[0], dev).free()                   # first-use setup (pinned buffers, streams)
         t0 = time.perf_counter()
-        qts = [c.tensor(f"blk.{i}.weight", dev) for i in range(count)]
+        qts = [c.tensor(nm, dev) for nm in names]
         dt_file = time.perf_counter() - t0
+        del qts
+        t0 = time.perf_counter()
+        qts = c.tensors(names, dev)
+        dt_batch = time.perf_counter() - t0
         c.close()
-    ok = all(np.array_equal(q.data(), r) for q, r in zip(qts[:1], raw[:1]))
+    ok = all(np.array_equal(qts[nm].data(), r) for nm, r in zip(names[:2], raw[:2]))
     del qts
     t0 = time.perf_counter()
     qts = [mold_amd.QTensor.from_blocks(dev, t, (n, k), r) for r in raw]
@@ -344,7 +365,6 @@ def bench_upload(dev, args):
     del qts
     # FP8 E4M3 -> Q8_0 on the device (the FP8 checkpoint cache producer's quantize step)
     import ctypes
-    import torch
     from mold_amd import _lib
     fn, fk = 21504, 3072
     src = torch.randint(0, 126, (fn, fk), dtype=torch.uint8, device="cuda")
@@ -359,9 +379,13 @@ def bench_upload(dev, args):
     return {"bytes": count * nbytes, "tensors": count,
             "fp8_to_q8_0_ms": round(dt_fp8 * 1e3, 3), "fp8_to_q8_0_gbs": round(fn * fk / dt_fp8 / 1e9, 1),
             "gguf_file_gbs": round(count * nbytes / dt_file / 1e9, 2),
-            "host_buffer_gbs": round(count * nbytes / dt_host / 1e9, 2), "readback_identical": bool(ok),
-            "what": "mq_gguf_load_tensor over a freshly written file (page cache: PCIe + pipeline, not disk), "
-                    "pinned 16 MiB chunks double-buffered; host_buffer = mq_qtensor_upload from pageable numpy; "
+            "gguf_file_batched_gbs": round(count * nbytes / dt_batch / 1e9, 2),
+            "host_buffer_gbs": round(count * nbytes / dt_host / 1e9, 2),
+            "pinned_h2d_ceiling_gbs": round(pinned_gbs, 2), "readback_identical": bool(ok),
+            "what": "GGUF file (page cache: PCIe + pipeline, not disk) -> device, 8 Q4_K [21504, 3072] tensors: "
+                    "gguf_file = mq_gguf_load_tensor per tensor, gguf_file_batched = one mq_gguf_load_tensors call "
+                    "(VarBuilder::from_gguf); host_buffer = mq_qtensor_upload from pageable numpy; "
+                    "pinned_h2d_ceiling = torch copy of one tensor's bytes from pinned host memory, same process; "
                     "fp8_to_q8_0: mq_quantize_fp8 of a device-resident FP8 E4M3 [21504, 3072] to Q8_0 including the "
                     "repack and the synchronization (GB/s of FP8 input)"}
 

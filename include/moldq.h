@@ -246,11 +246,21 @@ int mq_gguf_tensor_info(const mq_gguf *g, int64_t index, const char **name, int 
                         int *n_dims, int64_t dims[4], uint64_t *file_offset, size_t *nbytes);
 /* Read a tensor from the file and upload it (content.tensor(reader, name,
  * device), crates/mold-inference/src/flux/lora.rs:721-723): rows = the
- * product of ne[1..], k = ne[0]; block types and dense F32 / F16 / BF16.  The
- * file is read in 16 MiB chunks into two pinned host buffers in turn, each
- * copied to the device asynchronously while the next is read, then repacked
- * on the device (block types).  Synchronous. */
+ * product of ne[1..], k = ne[0]; block types and dense F32 / F16 / BF16.
+ * Several host threads read the file in chunks into pinned buffers of their
+ * own, each chunk copied to the device asynchronously while the thread reads
+ * its next one; block types are then repacked on the device.  Synchronous. */
 int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out);
+/* Upload `count` tensors of the file (indices into its tensor table, any
+ * order) into out[0..count): what candle's quantized VarBuilder::from_gguf
+ * (path, device) does for a whole model (crates/mold-inference/src/flux/
+ * pipeline.rs:976, qwen_image/pipeline.rs:936), each tensor as
+ * mq_gguf_load_tensor makes it.  One tensor's repack overlaps the next one's
+ * file read and copy (two device staging buffers of the largest tensor's
+ * size).  Synchronous; on failure every out[i] is NULL and nothing stays
+ * allocated. */
+int mq_gguf_load_tensors(mq_ctx *ctx, const mq_gguf *g, const int64_t *indices, int64_t count,
+                         mq_qtensor **out);
 /* The tensor's raw bytes as stored (any type, dense F32/F16/BF16 included)
  * into host memory; nbytes must equal the tensor's size.  What mold reads
  * with content.tensor(&mut file, name, &Device::Cpu) when it copies tensors

@@ -53,6 +53,7 @@ SIGNATURES = {
                                    ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(ctypes.c_uint64),
                                    ctypes.POINTER(_sz)]),
     "mq_gguf_load_tensor": (_int, [_vp, _vp, _i64, _pp]),
+    "mq_gguf_load_tensors": (_int, [_vp, _vp, _vp, _i64, _vp]),
     "mq_gguf_read_tensor": (_int, [_vp, _i64, _vp, _sz]),
     "mq_gguf_version": (_int, [_vp]),
     "mq_gguf_kv_count": (_i64, [_vp]),

@@ -1,13 +1,16 @@
 // mq_api.hip — the C ABI declared in include/moldq.h: contexts, HBM arena,
 // weight upload/download, dequantize and the quantized matmul dispatcher.
+#include <errno.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/moldq.h"
@@ -43,11 +46,15 @@ struct mq_ctx {
   // (mq_ctx_set_stream_tail_split).
   std::vector<hipStream_t> no_tail_split;
   size_t ws_floor = 0;  // mq_ctx_reserve_scratch: minimum size of every workspace
-  // Upload staging: a device buffer for raw GGUF blocks (grows, kept) and two
-  // pinned host buffers for file reads (allocated on the first GGUF load).
-  uint8_t *dstage = nullptr;
-  size_t dstage_size = 0;
-  uint8_t *pinned[2] = {nullptr, nullptr};
+  // Upload staging: device buffers for raw GGUF blocks (grow, kept; the
+  // second only for batched GGUF loads, which fill one while the other is
+  // repacked), and for each upload thread two pinned host buffers and a copy
+  // stream (allocated on the first large upload).  The repack runs on
+  // upload_stream.
+  uint8_t *dstage[2] = {};
+  size_t dstage_size[2] = {};
+  uint8_t *pinned[2 * mq::kUploadThreads] = {};
+  hipStream_t copy_streams[mq::kUploadThreads] = {};
   hipStream_t upload_stream = nullptr;
   // Device address of this GPU's copy of `scratch` (mq_qmatmul_noalloc).
   uint8_t *noalloc_scratch = nullptr;
@@ -327,24 +334,138 @@ int tensor_from_raw(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *ra
   return MQ_OK;
 }
 
-// The context's device staging buffer for raw blocks, at least `bytes` long.
-// Callers have synchronized the work that used it before (uploads, quantize
-// and download all return finished).
-int device_stage(mq_ctx *ctx, size_t bytes, uint8_t **out) {
-  if (bytes > ctx->dstage_size) {
-    if (ctx->dstage) {
-      HIP_TRY(hipFree(ctx->dstage), "free upload staging");
-      ctx->dstage = nullptr;
-      ctx->dstage_size = 0;
+// The context's device staging buffer `slot` (0 or 1) for raw blocks, at
+// least `bytes` long.  Callers have synchronized the work that used it before
+// (uploads, quantize and download all return finished).
+int device_stage(mq_ctx *ctx, size_t bytes, uint8_t **out, int slot = 0) {
+  uint8_t *&buf = ctx->dstage[slot];
+  size_t &size = ctx->dstage_size[slot];
+  if (bytes > size) {
+    if (buf) {
+      HIP_TRY(hipFree(buf), "free upload staging");
+      buf = nullptr;
+      size = 0;
     }
     const size_t sz = round_mib(bytes);
     void *p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
     if (e != hipSuccess) return fail(MQ_E_OOM, "hipMalloc(%zu) for upload staging failed: %s", sz, hipGetErrorString(e));
-    ctx->dstage = static_cast<uint8_t *>(p);
-    ctx->dstage_size = sz;
+    buf = static_cast<uint8_t *>(p);
+    size = sz;
   }
-  *out = ctx->dstage;
+  *out = buf;
+  return MQ_OK;
+}
+
+// Where a staged upload's bytes come from: an open file (pread at `offset`)
+// or host memory.
+struct UploadSource {
+  int fd = -1;
+  uint64_t offset = 0;
+  const uint8_t *host = nullptr;
+  // Fills dst with source bytes [pos, pos + len); false on a short read.
+  bool read(uint8_t *dst, size_t pos, size_t len) const {
+    if (host) {
+      memcpy(dst, host + pos, len);
+      return true;
+    }
+    size_t got = 0;
+    while (got < len) {
+      const ssize_t r = pread(fd, dst + got, len - got, (off_t)(offset + pos + got));
+      if (r < 0 && errno == EINTR) continue;
+      if (r <= 0) return false;
+      got += (size_t)r;
+    }
+    return true;
+  }
+};
+
+int upload_resources(mq_ctx *ctx) {
+  if (!ctx->upload_stream)
+    HIP_TRY(hipStreamCreateWithFlags(&ctx->upload_stream, hipStreamNonBlocking), "create upload stream");
+  for (auto &s : ctx->copy_streams)
+    if (!s) HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "create upload copy stream");
+  for (auto &p : ctx->pinned)
+    if (!p) HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&p), mq::kUploadChunk, hipHostMallocDefault), "hipHostMalloc");
+  return MQ_OK;
+}
+
+// Copies `nbytes` of `src` to device memory `dst` and returns once every byte
+// has landed.  The bytes are cut into T * rounds equal chunks (at most
+// kUploadChunk, at least 1 MiB unless the tensor is smaller, multiples of
+// 64 KiB), so every thread has the same work; chunk c belongs to thread
+// c % T.  A thread fills its two pinned buffers in turn (file read or memcpy,
+// the host-side cost that one thread cannot hide behind the PCIe copy) and
+// queues each chunk's copy on its own stream; a buffer is refilled only after
+// an event says its previous copy has left it.  The calling thread is thread 0.
+int staged_h2d(mq_ctx *ctx, const UploadSource &src, uint8_t *dst, size_t nbytes) {
+  if (nbytes == 0) return MQ_OK;
+  int rc = upload_resources(ctx);
+  if (rc) return rc;
+  constexpr size_t kGrain = size_t(64) << 10, kMinChunk = size_t(1) << 20;
+  const size_t nt_max = std::max<size_t>(1, std::min<size_t>(mq::kUploadThreads, (nbytes + kMinChunk - 1) / kMinChunk));
+  const size_t rounds = (nbytes + nt_max * mq::kUploadChunk - 1) / (nt_max * mq::kUploadChunk);
+  const size_t per = (nbytes + nt_max * rounds - 1) / (nt_max * rounds);
+  const size_t chunk = std::min(mq::kUploadChunk, (per + kGrain - 1) / kGrain * kGrain);
+  const size_t chunks = (nbytes + chunk - 1) / chunk;
+  const int nt = (int)std::min(nt_max, chunks);
+  struct Result {
+    int code = MQ_OK;
+    char msg[160] = {};
+  };
+  std::vector<Result> res(nt);
+  std::atomic<bool> stop{false};
+  auto work = [&](int t) {
+    Result &r = res[t];
+    auto bad = [&](int code, const char *what, size_t pos) {
+      r.code = code;
+      snprintf(r.msg, sizeof r.msg, "%s at byte %zu of a %zu-byte upload", what, pos, nbytes);
+      stop.store(true);
+    };
+    hipStream_t s = ctx->copy_streams[t];
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    if (hipSetDevice(ctx->device) != hipSuccess || hipEventCreateWithFlags(&ev[0], hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ev[1], hipEventDisableTiming) != hipSuccess) {
+      bad(MQ_E_HIP, "upload thread set-up failed", 0);
+    } else {
+      bool used[2] = {false, false};
+      int b = 0;
+      for (size_t c = (size_t)t; c < chunks && !stop.load(std::memory_order_relaxed); c += (size_t)nt, b ^= 1) {
+        const size_t pos = c * chunk, len = std::min(chunk, nbytes - pos);
+        uint8_t *buf = ctx->pinned[2 * t + b];
+        if (used[b] && hipEventSynchronize(ev[b]) != hipSuccess) {
+          bad(MQ_E_HIP, "upload event wait failed", pos);
+          break;
+        }
+        if (!src.read(buf, pos, len)) {
+          bad(MQ_E_IO, "short read", (size_t)src.offset + pos);
+          break;
+        }
+        if (hipMemcpyAsync(dst + pos, buf, len, hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipEventRecord(ev[b], s) != hipSuccess) {
+          bad(MQ_E_HIP, "async H2D copy failed", pos);
+          break;
+        }
+        used[b] = true;
+      }
+    }
+    // No copy may still read a pinned buffer once this call returns.
+    if (hipStreamSynchronize(s) != hipSuccess && r.code == MQ_OK) bad(MQ_E_HIP, "upload copy stream failed", 0);
+    for (auto e : ev)
+      if (e) (void)hipEventDestroy(e);
+  };
+  std::vector<std::thread> pool;
+  try {
+    for (int t = 1; t < nt; ++t) pool.emplace_back(work, t);
+  } catch (...) {  // fewer threads than asked for: stop the ones started
+    stop.store(true);
+    for (auto &th : pool) th.join();
+    return fail(MQ_E_HIP, "could not start upload threads");
+  }
+  work(0);
+  for (auto &th : pool) th.join();
+  for (const Result &r : res)
+    if (r.code != MQ_OK) return fail(r.code, "%s", r.msg);
   return MQ_OK;
 }
 
@@ -407,9 +528,12 @@ void mq_ctx_destroy(mq_ctx *ctx) {
   for (auto &w : ctx->ws)
     if (w.p) (void)hipFree(w.p);
   for (void *p : ctx->retired) (void)hipFree(p);
-  if (ctx->dstage) (void)hipFree(ctx->dstage);
+  for (auto *p : ctx->dstage)
+    if (p) (void)hipFree(p);
   for (auto *p : ctx->pinned)
     if (p) (void)hipHostFree(p);
+  for (auto s : ctx->copy_streams)
+    if (s) (void)hipStreamDestroy(s);
   if (ctx->upload_stream) (void)hipStreamDestroy(ctx->upload_stream);
   if (ctx->arena) (void)hipFree(ctx->arena);
   delete ctx;
@@ -490,7 +614,14 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
   uint8_t *st = nullptr;
   rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;
-  HIP_TRY(hipMemcpy(st, host_blocks, nbytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  if (nbytes > kUploadChunk) {  // large weights: the threaded pinned pipeline
+    UploadSource src;
+    src.host = static_cast<const uint8_t *>(host_blocks);
+    rc = staged_h2d(ctx, src, st, nbytes);
+    if (rc) return rc;
+  } else {
+    HIP_TRY(hipMemcpy(st, host_blocks, nbytes, hipMemcpyHostToDevice), "hipMemcpy H2D");
+  }
   rc = tensor_from_raw(ctx, dtype, n, k, st, nullptr, out);
   if (rc) return rc;
   hipError_t se = hipStreamSynchronize(nullptr);
@@ -688,69 +819,69 @@ int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_
 }  // extern "C"
 
 // ------------------------------------------------------------ GGUF upload
-// Host-side piece of mq_gguf_load_tensor (mq_gguf.cpp): the tensor's bytes go
-// from the file straight into two pinned host buffers in turn, each chunk is
-// copied to the device staging buffer asynchronously (the file read of chunk
-// i+1 overlaps the PCIe copy of chunk i), then the repack runs on the device.
+// Host-side piece of mq_gguf_load_tensor(s) (mq_gguf.cpp): each tensor's bytes
+// go from the file through the threaded pinned pipeline (staged_h2d) into a
+// device staging buffer, then the repack runs on the upload stream.  Tensors
+// alternate between two staging buffers, so tensor i's repack (and the next
+// tensor's hipMalloc) overlaps tensor i+1's file read and copy; a staging
+// buffer is refilled once the event after its last repack has fired.
 namespace mq {
 
-int upload_from_file(mq_ctx *ctx, int dtype, int64_t n, int64_t k, int fd, uint64_t offset, size_t nbytes,
-                     mq_qtensor **out) {
-  *out = nullptr;
-  int rc = check_weight_shape(dtype, n, k, nbytes);
-  if (rc) return rc;
+int upload_from_file(mq_ctx *ctx, int fd, const UploadJob *jobs, int64_t count, mq_qtensor **out) {
+  for (int64_t i = 0; i < count; ++i) out[i] = nullptr;
+  size_t most = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const int rc = check_weight_shape(jobs[i].dtype, jobs[i].n, jobs[i].k, jobs[i].nbytes);
+    if (rc) return rc;
+    most = std::max(most, jobs[i].nbytes);
+  }
+  if (count == 0) return MQ_OK;
   DeviceGuard g(ctx->device);
-  if (!ctx->upload_stream)
-    HIP_TRY(hipStreamCreateWithFlags(&ctx->upload_stream, hipStreamNonBlocking), "create upload stream");
-  for (auto &p : ctx->pinned)
-    if (!p) HIP_TRY(hipHostMalloc(reinterpret_cast<void **>(&p), kUploadChunk, hipHostMallocDefault), "hipHostMalloc");
-  uint8_t *st = nullptr;
-  rc = device_stage(ctx, nbytes, &st);
+  uint8_t *st[2] = {nullptr, nullptr};
+  for (int b = 0; b < (count > 1 ? 2 : 1); ++b) {
+    const int rc = device_stage(ctx, most, &st[b], b);
+    if (rc) return rc;
+  }
+  int rc = upload_resources(ctx);
   if (rc) return rc;
-  hipEvent_t ev[2] = {nullptr, nullptr};
-  for (auto &e : ev)
+  hipEvent_t done[2] = {nullptr, nullptr};
+  for (auto &e : done)
     if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
-      for (auto &d : ev)
+      for (auto &d : done)
         if (d) (void)hipEventDestroy(d);
-      return fail(MQ_E_HIP, "event create failed");
+      return fail(MQ_E_HIP, "upload event create failed");
     }
-  bool used[2] = {false, false};
-  int result = MQ_OK;
-  size_t done = 0;
-  for (int i = 0; done < nbytes; i ^= 1) {
-    const size_t len = std::min(kUploadChunk, nbytes - done);
-    if (used[i] && hipEventSynchronize(ev[i]) != hipSuccess) {  // buffer i's previous copy has left it
-      result = fail(MQ_E_HIP, "upload event wait failed");
+  bool pending[2] = {false, false};
+  int64_t made = 0;
+  for (; made < count; ++made) {
+    const UploadJob &j = jobs[made];
+    const int b = (int)(made & 1);
+    if (pending[b] && hipEventSynchronize(done[b]) != hipSuccess) {  // its last repack has read it
+      rc = fail(MQ_E_HIP, "upload staging event wait failed");
       break;
     }
-    size_t got = 0;
-    while (got < len) {
-      const ssize_t r = pread(fd, ctx->pinned[i] + got, len - got, (off_t)(offset + done + got));
-      if (r <= 0) break;
-      got += (size_t)r;
-    }
-    if (got != len) {
-      result = fail(MQ_E_IO, "short read at byte %llu of a %zu-byte tensor", (unsigned long long)(offset + done), nbytes);
+    UploadSource src;
+    src.fd = fd;
+    src.offset = j.offset;
+    rc = staged_h2d(ctx, src, st[b], j.nbytes);
+    if (rc) break;
+    rc = tensor_from_raw(ctx, j.dtype, j.n, j.k, st[b], ctx->upload_stream, &out[made]);
+    if (rc) break;
+    if (hipEventRecord(done[b], ctx->upload_stream) != hipSuccess) {
+      rc = fail(MQ_E_HIP, "upload staging event record failed");
       break;
     }
-    if (hipMemcpyAsync(st + done, ctx->pinned[i], len, hipMemcpyHostToDevice, ctx->upload_stream) != hipSuccess ||
-        hipEventRecord(ev[i], ctx->upload_stream) != hipSuccess) {
-      result = fail(MQ_E_HIP, "async H2D copy failed");
-      break;
-    }
-    used[i] = true;
-    done += len;
+    pending[b] = true;
   }
-  if (result == MQ_OK) result = tensor_from_raw(ctx, dtype, n, k, st, ctx->upload_stream, out);
   const hipError_t se = hipStreamSynchronize(ctx->upload_stream);
-  for (auto &e : ev) (void)hipEventDestroy(e);
-  if (result != MQ_OK) return result;
-  if (se != hipSuccess) {
-    mq_qtensor_free(*out);
-    *out = nullptr;
-    return hip_fail(se, "upload synchronize");
-  }
-  return MQ_OK;
+  for (auto e : done) (void)hipEventDestroy(e);
+  if (rc == MQ_OK && se != hipSuccess) rc = hip_fail(se, "upload synchronize");
+  if (rc != MQ_OK)
+    for (int64_t i = 0; i < count; ++i) {
+      mq_qtensor_free(out[i]);
+      out[i] = nullptr;
+    }
+  return rc;
 }
 
 }  // namespace mq

@@ -407,18 +407,43 @@ int mq_gguf_kv_str(const mq_gguf *g, int64_t index, uint64_t elem, const char **
   return MQ_OK;
 }
 
+int mq_gguf_load_tensors(mq_ctx *ctx, const mq_gguf *g, const int64_t *indices, int64_t count, mq_qtensor **out) {
+  if (!g || !out || count < 0 || (count > 0 && !indices))
+    return gfail(MQ_E_INVALID, "mq_gguf_load_tensors: bad argument");
+  for (int64_t i = 0; i < count; ++i) out[i] = nullptr;
+  if (!ctx) return gfail(MQ_E_INVALID, "mq_gguf_load_tensors: NULL ctx");
+  if (count == 0) return MQ_OK;
+  std::vector<mq::UploadJob> jobs;
+  const int rj = no_throw("mq_gguf_load_tensors", [&] {
+    jobs.resize((size_t)count);
+    return MQ_OK;
+  });
+  if (rj) return rj;
+  for (int64_t i = 0; i < count; ++i) {
+    const int64_t index = indices[i];
+    if (index < 0 || index >= (int64_t)g->tensors.size())
+      return gfail(MQ_E_INVALID, "mq_gguf_load_tensors: index %lld out of range", (long long)index);
+    const TensorInfo &t = g->tensors[(size_t)index];
+    mq::UploadJob &j = jobs[(size_t)i];
+    j.dtype = t.dtype;
+    j.n = 1;
+    for (int d = 1; d < t.n_dims; ++d) j.n *= t.dims[d];
+    j.k = t.dims[0];
+    j.offset = t.offset;
+    j.nbytes = t.nbytes;
+  }
+  const int fd = open(g->path.c_str(), O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return gfail(MQ_E_IO, "cannot reopen %s", g->path.c_str());
+  const int rc = mq::upload_from_file(ctx, fd, jobs.data(), count, out);
+  close(fd);
+  return rc;
+}
+
 int mq_gguf_load_tensor(mq_ctx *ctx, const mq_gguf *g, int64_t index, mq_qtensor **out) {
   if (!g || !out || index < 0 || index >= (int64_t)g->tensors.size())
     return gfail(MQ_E_INVALID, "mq_gguf_load_tensor: bad argument");
-  const TensorInfo &t = g->tensors[(size_t)index];
-  int64_t rows = 1;
-  for (int d = 1; d < t.n_dims; ++d) rows *= t.dims[d];
   if (!ctx) return gfail(MQ_E_INVALID, "mq_gguf_load_tensor: NULL ctx");
-  const int fd = open(g->path.c_str(), O_RDONLY | O_CLOEXEC);
-  if (fd < 0) return gfail(MQ_E_IO, "cannot reopen %s", g->path.c_str());
-  const int rc = mq::upload_from_file(ctx, t.dtype, rows, t.dims[0], fd, t.offset, t.nbytes, out);
-  close(fd);
-  return rc;
+  return mq_gguf_load_tensors(ctx, g, &index, 1, out);
 }
 
 }  // extern "C"

@@ -169,36 +169,41 @@ class FluxParams:
         FLUX tensor names, `<linear>.weight` / `<linear>.bias`, norm `.scale`s,
         `img_in`), loaded the way mold's `VarBuilder::from_gguf` does
         (crates/mold-inference/src/flux/pipeline.rs:976-977): every tensor goes to
-        the device through libmoldq (mq_gguf_load_tensor), block-type weights stay
-        quantized, and dense tensors (F32 / F16 / BF16) are dequantized on the
-        device to the dtypes the step uses (f32 biases, bf16 norm scales and
-        img_in weight).  No tensor byte passes through the host here except on
-        the upload itself."""
+        the device through libmoldq in one pipelined call (mq_gguf_load_tensors),
+        block-type weights stay quantized, and dense tensors (F32 / F16 / BF16)
+        are dequantized on the device to the dtypes the step uses (f32 biases,
+        bf16 norm scales and img_in weight).  No tensor byte passes through the
+        host here except on the upload itself."""
         import torch
         from . import gguf
+        need = {}
+        for name, (n, k, has_bias) in linear_shapes(cfg).items():
+            need[name + ".weight"] = (n, k)
+            if has_bias:
+                need[name + ".bias"] = (n,)
+        need.update(dense_shapes(cfg))
         c = gguf.Content.read(path)
         try:
-            def load(name, shape):
+            for name in need:
                 if name not in c.tensor_infos:
                     raise KeyError(f"{path}: tensor {name} missing")
-                qt = c.tensor(name, device)
-                want = (int(np.prod(shape[:-1])) if len(shape) > 1 else 1, shape[-1])
-                if qt.shape != want:
-                    raise ValueError(f"{name}: stored as {qt.shape}, the config needs {tuple(shape)}")
-                return qt
-
-            lin, dense = {}, {}
-            for name, (n, k, has_bias) in linear_shapes(cfg).items():
-                qt = load(name + ".weight", (n, k))
-                if not qt.dtype().is_quantized:
-                    raise ValueError(f"{name}.weight is dense {qt.dtype().name}; the step runs quantized linears")
-                bias = load(name + ".bias", (n,)).dequantize(torch.float32).reshape(n) if has_bias else None
-                lin[name] = Linear(qt, bias)
-            for name, shape in dense_shapes(cfg).items():
-                dt = torch.float32 if name.endswith(".bias") else torch.bfloat16
-                dense[name] = load(name, shape).dequantize(dt).reshape(shape)
+            qts = c.tensors(need.keys(), device)
         finally:
             c.close()
+        for name, shape in need.items():
+            want = (int(np.prod(shape[:-1])) if len(shape) > 1 else 1, shape[-1])
+            if qts[name].shape != want:
+                raise ValueError(f"{name}: stored as {qts[name].shape}, the config needs {tuple(shape)}")
+        lin, dense = {}, {}
+        for name, (n, k, has_bias) in linear_shapes(cfg).items():
+            qt = qts[name + ".weight"]
+            if not qt.dtype().is_quantized:
+                raise ValueError(f"{name}.weight is dense {qt.dtype().name}; the step runs quantized linears")
+            bias = qts[name + ".bias"].dequantize(torch.float32).reshape(n) if has_bias else None
+            lin[name] = Linear(qt, bias)
+        for name, shape in dense_shapes(cfg).items():
+            dt = torch.float32 if name.endswith(".bias") else torch.bfloat16
+            dense[name] = qts[name].dequantize(dt).reshape(shape)
         return FluxParams(cfg, lin, dense)
 
     def quantized_bytes(self) -> int:

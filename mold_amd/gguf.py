@@ -109,6 +109,24 @@ class Content:
         check(_lib.load().mq_gguf_load_tensor(device.handle, self._h, self._index[name], ctypes.byref(h)))
         return QTensor(device, h)
 
+    def tensors(self, names, device: Device) -> Dict[str, QTensor]:
+        """Upload several tensors in one pipelined call (candle's quantized
+        VarBuilder::from_gguf(path, device), crates/mold-inference/src/flux/
+        pipeline.rs:976, which loads every tensor of the file): {name: QTensor},
+        in the order given."""
+        names = list(names)
+        for n in names:
+            if n not in self._index:
+                raise KeyError(n)
+        idx = (ctypes.c_int64 * max(1, len(names)))(*[self._index[n] for n in names])
+        outs = (ctypes.c_void_p * max(1, len(names)))()
+        check(_lib.load().mq_gguf_load_tensors(device.handle, self._h, idx, len(names), outs))
+        return {n: QTensor(device, ctypes.c_void_p(outs[i])) for i, n in enumerate(names)}
+
+    def var_builder(self, device: Device) -> Dict[str, QTensor]:
+        """Every tensor of the file on the device, by name (VarBuilder::from_gguf)."""
+        return self.tensors(self.tensor_infos.keys(), device)
+
     def tensor_bytes(self, name: str) -> np.ndarray:
         """The tensor's stored bytes (any type), as uint8."""
         if name not in self._index:

@@ -91,6 +91,18 @@ void walk(mq_gguf *g, bool strict) {
     mq_qtensor *qt = nullptr;
     CHECK(mq_gguf_load_tensor(nullptr, g, i, &qt) != MQ_OK);  // no device here
   }
+  // the batched load builds every job, then reaches the (device-less) upload
+  std::vector<int64_t> idx;
+  for (int64_t i = 0; i < nt; ++i) idx.push_back(nt - 1 - i);
+  std::vector<mq_qtensor *> outs(idx.size() + 2, reinterpret_cast<mq_qtensor *>(&idx));
+  int fake = 0;
+  mq_ctx *ctx = reinterpret_cast<mq_ctx *>(&fake);
+  CHECK(mq_gguf_load_tensors(ctx, g, idx.data(), nt, outs.data()) == (nt ? MQ_E_UNSUPPORTED : MQ_OK));
+  for (int64_t i = 0; i < nt; ++i) CHECK(outs[(size_t)i] == nullptr);
+  const int64_t bad[2] = {0, nt};
+  CHECK(mq_gguf_load_tensors(ctx, g, bad, 2, outs.data()) == MQ_E_INVALID);
+  CHECK(mq_gguf_load_tensors(ctx, g, nullptr, 1, outs.data()) == MQ_E_INVALID);
+  CHECK(mq_gguf_load_tensors(nullptr, g, idx.data(), nt, outs.data()) == MQ_E_INVALID);
   CHECK(mq_gguf_tensor_info(g, nt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr) == MQ_E_INVALID);
   CHECK(mq_gguf_kv_info(g, nkv, nullptr, nullptr, nullptr, nullptr) == MQ_E_INVALID);
 }

@@ -17,8 +17,8 @@ int set_error(int code, const char *msg) {
   g_err = msg;
   return code;
 }
-int upload_from_file(mq_ctx *, int, int64_t, int64_t, int, uint64_t, size_t, mq_qtensor **out) {
-  *out = nullptr;
+int upload_from_file(mq_ctx *, int, const UploadJob *, int64_t count, mq_qtensor **out) {
+  for (int64_t i = 0; i < count; ++i) out[i] = nullptr;
   return set_error(MQ_E_UNSUPPORTED, "no device in the sanitizer build");
 }
 }  // namespace mq

@@ -33,6 +33,19 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) == set(_lib.SIGNATURES)
 
 
+def test_library_exports_nothing_but_the_c_abi():
+    """The dynamic symbol table holds the header's mq_* functions and no internal
+    C++ name, so two builds loaded into one process cannot bind to each other's
+    internals."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not on PATH")
+    out = subprocess.run([nm, "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    names = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert names == set(_declared_symbols()), sorted(names ^ set(_declared_symbols()))[:10]
+
 def test_version_and_type_table():
     lib = _lib.load()
     assert lib.mq_version() == 1

@@ -541,6 +541,61 @@ def test_gguf_file_to_device(dev, torch, tmp_path):
     c.close()
 
 
+def test_gguf_batched_load_equals_one_by_one(dev, torch, tmp_path):
+    """mq_gguf_load_tensors (VarBuilder::from_gguf): every type, sizes from one block
+    to several chunks per upload thread (a 37 MB Q4_K), dense tensors between them,
+    a tensor named twice, any order; the same bytes as a load of each tensor alone
+    and as the file holds.  A bad index fails the whole call and leaves no tensor."""
+    _say("gguf batched load")
+    from mold_amd import gguf
+    from mold_amd._lib import MQ_E_INVALID
+    rng = np.random.default_rng(11)
+    tensors = [("big", GgmlDType.Q4_K, (21504, 3072), _random_blocks(int(GgmlDType.Q4_K), 21504, 3072, 2))]
+    for i, t in enumerate(TYPES):
+        n, k = (1, 256) if i % 3 == 0 else (257 + 64 * i, 1024 + 512 * (i % 2))
+        tensors.append((f"w{i}", t, (n, k), _random_blocks(int(t), n, k, 20 + i)))
+        tensors.append((f"d{i}", GgmlDType.F32, (1, 7 + i), rng.integers(0, 256, 4 * (7 + i), dtype=np.uint8)))
+    tensors.append(("bf", GgmlDType.BF16, (3072, 1000), rng.integers(0, 256, 3072 * 2000, dtype=np.uint8)))
+    p = str(tmp_path / "many.gguf")
+    gguf.write(p, [(nm, t, shape, b) for nm, t, shape, b in tensors])
+    c = gguf.Content.read(p)
+    try:
+        names = [nm for nm, *_ in tensors]
+        order = [names[j] for j in rng.permutation(len(names))] + ["w3"]
+        got = c.tensors(order, dev)
+        assert list(got) == list(dict.fromkeys(order))
+        for nm, t, shape, b in tensors:
+            qt = got[nm]
+            assert qt.dtype() == t and qt.shape == shape, nm
+            assert np.array_equal(qt.data(), b.reshape(-1)), nm
+            one = c.tensor(nm, dev)
+            assert np.array_equal(one.data(), qt.data()), nm
+            one.free()
+        allt = c.var_builder(dev)
+        assert set(allt) == set(names)
+        assert np.array_equal(allt["big"].data(), tensors[0][3].reshape(-1))
+        del got, allt
+        lib = mold_amd._lib.load()
+        idx = (ctypes.c_int64 * 3)(0, 1, len(names))
+        outs = (ctypes.c_void_p * 3)(1, 2, 3)
+        assert lib.mq_gguf_load_tensors(dev.handle, c._h, idx, 3, outs) == MQ_E_INVALID
+        assert all(o is None for o in outs)
+        assert lib.mq_gguf_load_tensors(dev.handle, c._h, idx, 0, outs) == 0
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q8_0], ids=lambda t: t.name)
+def test_large_host_upload_through_the_pipeline(dev, t):
+    """Weights above one pinned chunk go through the threaded upload pipeline:
+    byte-identical, including a size that is not a multiple of the chunk."""
+    n, k = 20001, 4096
+    _say(f"large host upload {t.name} [{n},{k}]")
+    blocks = _random_blocks(int(t), n, k, 9)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    assert np.array_equal(qt.data(), blocks.reshape(-1))
+
+
 def test_arena_residency(torch):
     _say("arena")
     d = mold_amd.Device(0)
