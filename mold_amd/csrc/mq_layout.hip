@@ -1,47 +1,110 @@
 // mq_layout.hip — GGUF blocks <-> device tiled-planar layout (see mq_common.h),
 // dense dequantize, and the f32 -> bf16 activation staging used by the GEMM.
+#include <utility>
+
 #include "mq_kernels.h"
 
 namespace mq {
 
-// One thread per GGUF byte (grid-stride).  inverse=false: raw -> tiled, over
-// the padded row count so the rows past n of the last tile are written as
-// zeros (no separate clear); inverse=true: tiled -> raw over the n real rows.
-// Upload/download only, never on the hot path.
-template <int TYPE>
-__global__ void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, Geo g,
-                              int64_t total, int inverse) {
-  constexpr TypeInfo ti = type_info(TYPE);
-  const int64_t row_bytes = g.nb * ti.ts;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = i / row_bytes;
-    const int64_t rem = i - n * row_bytes;
-    const int64_t b = rem / ti.ts;
-    const int j = (int)(rem - b * ti.ts);
-    int f = 0;
+// Largest power of two (at most 16) dividing v.
+constexpr int pow2_div(int v) {
+  int a = 1;
+  while (a < 16 && v % (2 * a) == 0) a *= 2;
+  return a;
+}
+
+template <int U>
+struct UnitT;
+template <> struct UnitT<1> { using type = uint8_t; };
+template <> struct UnitT<2> { using type = uint16_t; };
+template <> struct UnitT<4> { using type = uint32_t; };
+template <> struct UnitT<8> { using type = uint2; };
+template <> struct UnitT<16> { using type = uint4; };
+
+// Moves SIZE bytes in units of U bytes (both sides U-aligned); zero: store zeros.
+template <int U, int SIZE>
+__device__ __forceinline__ void move_bytes(uint8_t *d, const uint8_t *s, bool zero) {
+  using T = typename UnitT<U>::type;
 #pragma unroll
-    for (int q = 1; q < ti.nf; ++q)
-      if (j >= ti.f[q].off) f = q;
-    const int64_t off = field_offset(g.plane[f], ti.f[f].size, g.nb, n / kRowTile, b,
-                                     (int)(n % kRowTile), j - ti.f[f].off);
-    if (inverse) dst[i] = src[off];
-    else dst[off] = n < g.n ? src[i] : uint8_t(0);
+  for (int i = 0; i < SIZE / U; ++i) {
+    T v{};
+    if (!zero) v = reinterpret_cast<const T *>(s)[i];
+    reinterpret_cast<T *>(d)[i] = v;
+  }
+}
+
+// Field F of block (tile t, block b), row r: between the raw block at `raw`
+// and the tiled planes at `tiled`.  A chunked field moves as 16-byte columns
+// (the wave's 64 rows of one column are one contiguous KiB), a record as one
+// run; units are the largest both sides' alignment allows.  With ALIGNED (the
+// raw buffer starts on 16 bytes) the raw side's alignment is fixed by the
+// block size and the field offset, since rows start at multiples of the
+// block size; otherwise the raw side moves bytes.
+template <int TYPE, bool ALIGNED, int F>
+__device__ __forceinline__ void repack_field(uint8_t *raw, uint8_t *tiled, const Geo &g, int64_t tb, int r,
+                                             bool inverse, bool zero) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  constexpr int size = ti.f[F].size, off = ti.f[F].off;
+  constexpr int ua = !ALIGNED ? 1
+                     : pow2_div(ti.ts) < pow2_div(off == 0 ? 16 : off) ? pow2_div(ti.ts)
+                                                                        : pow2_div(off == 0 ? 16 : off);
+  if constexpr (size % 16 == 0) {
+#pragma unroll
+    for (int c = 0; c < size / 16; ++c) {
+      uint8_t *tp = tiled + g.plane[F] + ((tb * (size / 16) + c) * kRowTile + r) * 16;
+      uint8_t *rp = raw + off + 16 * c;
+      if (inverse) move_bytes<ua, 16>(rp, tp, false);
+      else move_bytes<ua, 16>(tp, rp, zero);
+    }
+  } else {
+    constexpr int u = ua < pow2_div(size) ? ua : pow2_div(size);
+    uint8_t *tp = tiled + g.plane[F] + (tb * kRowTile + r) * size;
+    uint8_t *rp = raw + off;
+    if (inverse) move_bytes<u, size>(rp, tp, false);
+    else move_bytes<u, size>(tp, rp, zero);
+  }
+}
+
+// One thread per (row, block); a wave holds the 64 rows of one tile for one
+// block, so every write of the tiled side (and every read, inverse) is a
+// contiguous run and each thread reads its own block's bytes.  inverse=false:
+// raw -> tiled over the padded rows, the rows past n of the last tile written
+// as zeros (no separate clear); inverse=true: tiled -> raw over the n real
+// rows.  Upload/download only, never on the hot path.
+template <int TYPE, bool ALIGNED>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                     Geo g, int inverse) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  const int r = threadIdx.x & (kRowTile - 1);
+  const int64_t pairs = g.ntiles * g.nb, row_bytes = g.nb * ti.ts;
+  uint8_t *raw_base = inverse ? dst : const_cast<uint8_t *>(src);
+  uint8_t *tiled = inverse ? const_cast<uint8_t *>(src) : dst;
+  for (int64_t tb = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); tb < pairs; tb += (int64_t)gridDim.x * 4) {
+    const int64_t t = tb / g.nb, b = tb - t * g.nb;
+    const int64_t n = t * kRowTile + r;
+    const bool real = n < g.n;
+    if (inverse && !real) continue;
+    uint8_t *raw = raw_base + (real ? n : 0) * row_bytes + b * ti.ts;
+    [&]<int... F>(std::integer_sequence<int, F...>) {
+      (repack_field<TYPE, ALIGNED, F>(raw, tiled, g, tb, r, inverse != 0, !real), ...);
+    }(std::make_integer_sequence<int, ti.nf>{});
   }
 }
 
 hipError_t launch_repack(int type, const void *src, void *dst, const Geo &g, bool inverse,
                          hipStream_t stream) {
-  const TypeInfo ti = type_info(type);
-  const int64_t total = (inverse ? g.n : g.ntiles * kRowTile) * g.nb * ti.ts;
-  if (total == 0) return hipSuccess;
-  const int threads = 256;
-  const int64_t want = (total + threads - 1) / threads;
+  const int64_t pairs = g.ntiles * g.nb;
+  if (pairs == 0) return hipSuccess;
+  const int64_t want = (pairs + 3) / 4;
   const int blocks = (int)(want < 65536 ? want : 65536);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(inverse ? dst : src)) & 15) == 0;
   bool ok = dispatch_type(type, [&]<int T>() {
-    hipLaunchKernelGGL(repack_kernel<T>, dim3(blocks), dim3(threads), 0, stream,
-                       static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), g, total,
-                       inverse ? 1 : 0);
+    if (aligned)
+      hipLaunchKernelGGL((repack_kernel<T, true>), dim3(blocks), dim3(256), 0, stream,
+                         static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), g, inverse ? 1 : 0);
+    else
+      hipLaunchKernelGGL((repack_kernel<T, false>), dim3(blocks), dim3(256), 0, stream,
+                         static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), g, inverse ? 1 : 0);
   });
   if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();

@@ -585,6 +585,24 @@ def test_gguf_batched_load_equals_one_by_one(dev, torch, tmp_path):
         c.close()
 
 
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+def test_from_device_blocks_at_any_alignment(dev, torch, t):
+    """mq_qtensor_from_device on GGUF blocks that start 0, 1, 2, 6 and 16 bytes into
+    a device buffer: the repack reads byte by byte where the start is not 16-byte
+    aligned; the tensor equals the host upload's, and downloads its own bytes."""
+    n, k = 130, 2 * O.block_size(int(t))
+    blocks = _random_blocks(int(t), n, k, 31).reshape(-1)
+    ref = QTensor.from_blocks(dev, t, (n, k), blocks)
+    buf = torch.zeros(blocks.size + 64, dtype=torch.uint8, device="cuda")
+    for shift in (0, 1, 2, 6, 16):
+        _say(f"from_device {t.name} shift {shift}")
+        buf[shift:shift + blocks.size] = torch.from_numpy(blocks).cuda()
+        qt = QTensor.from_device_blocks(dev, t, (n, k), buf[shift:shift + blocks.size])
+        torch.cuda.synchronize()
+        assert np.array_equal(qt.data(), blocks), shift
+        assert _bits_equal(qt.dequantize().cpu().numpy(), ref.dequantize().cpu().numpy()), shift
+
+
 @pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q8_0], ids=lambda t: t.name)
 def test_large_host_upload_through_the_pipeline(dev, t):
     """Weights above one pinned chunk go through the threaded upload pipeline:
