@@ -149,6 +149,13 @@ int mq_quantize_fp8(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *sr
 /* Read the weight back as GGUF blocks (byte-identical to what was uploaded).
  * Synchronous. */
 int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, size_t nbytes);
+/* Stack `count` tensors of one type and k by rows into a new tensor: row r of
+ * parts[i] becomes row n_0 + .. + n_(i-1) + r.  No candle counterpart: the
+ * stacked adaLN modulation weight of a DiT step (every block's modulation
+ * linear reads the same conditioning vector, crates/mold-inference/src/flux/
+ * offload.rs:143-156, qwen_image/quantized_transformer.rs:869-881), built on
+ * the device without a host round trip.  The parts stay valid.  Synchronous. */
+int mq_qtensor_concat_rows(mq_ctx *ctx, const mq_qtensor *const *parts, int64_t count, mq_qtensor **out);
 void mq_qtensor_free(mq_qtensor *w);
 /* QTensor::dtype() / shape / storage_size_in_bytes(). */
 int mq_qtensor_info(const mq_qtensor *w, int *dtype, int64_t *n, int64_t *k,

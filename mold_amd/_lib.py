@@ -34,6 +34,7 @@ SIGNATURES = {
     "mq_lora_apply": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _int, ctypes.c_float, _vp]),
     "mq_quantize_fp8": (_int, [_vp, _int, _i64, _i64, _vp, _i64, ctypes.c_float, _vp, _pp]),
     "mq_qtensor_download": (_int, [_vp, _vp, _vp, _sz]),
+    "mq_qtensor_concat_rows": (_int, [_vp, _vp, _i64, _pp]),
     "mq_qtensor_free": (None, [_vp]),
     "mq_qtensor_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_i64), ctypes.POINTER(_i64),
                                ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),

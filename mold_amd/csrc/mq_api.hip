@@ -711,6 +711,49 @@ int mq_qtensor_download(mq_ctx *ctx, const mq_qtensor *w, void *host_blocks, siz
   return MQ_OK;
 }
 
+int mq_qtensor_concat_rows(mq_ctx *ctx, const mq_qtensor *const *parts, int64_t count, mq_qtensor **out) {
+  if (!ctx || !parts || !out || count <= 0) return fail(MQ_E_INVALID, "mq_qtensor_concat_rows: bad argument");
+  *out = nullptr;
+  int64_t n = 0;
+  size_t bytes = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const mq_qtensor *p = parts[i];
+    if (!p) return fail(MQ_E_INVALID, "mq_qtensor_concat_rows: part %lld is NULL", (long long)i);
+    if (p->ctx != ctx) return fail(MQ_E_INVALID, "mq_qtensor_concat_rows: part %lld belongs to another context", (long long)i);
+    if (p->dtype != parts[0]->dtype || p->k != parts[0]->k)
+      return fail(MQ_E_INVALID, "mq_qtensor_concat_rows: part %lld is type %d with k = %lld, part 0 type %d with k = %lld",
+                  (long long)i, p->dtype, (long long)p->k, parts[0]->dtype, (long long)parts[0]->k);
+    n += p->n;
+    bytes += p->gguf_bytes;
+  }
+  const int dtype = parts[0]->dtype;
+  int rc = check_weight_shape(dtype, n, parts[0]->k, bytes);
+  if (rc) return rc;
+  DeviceGuard g(ctx->device);
+  uint8_t *st = nullptr;
+  rc = device_stage(ctx, bytes, &st);
+  if (rc) return rc;
+  // every part's GGUF bytes, in order, into the staging buffer (the inverse
+  // repack writes its n real rows), then one repack of the whole
+  size_t off = 0;
+  for (int64_t i = 0; i < count; ++i) {
+    const mq_qtensor *p = parts[i];
+    const hipError_t e = is_dense(dtype) ? hipMemcpyAsync(st + off, p->data, p->gguf_bytes, hipMemcpyDeviceToDevice, nullptr)
+                                         : launch_repack(dtype, p->data, st + off, p->geo, true, nullptr);
+    if (e != hipSuccess) return hip_fail(e, "concat: part to GGUF blocks");
+    off += p->gguf_bytes;
+  }
+  rc = tensor_from_raw(ctx, dtype, n, parts[0]->k, st, nullptr, out);
+  if (rc) return rc;
+  const hipError_t se = hipStreamSynchronize(nullptr);
+  if (se != hipSuccess) {
+    mq_qtensor_free(*out);
+    *out = nullptr;
+    return hip_fail(se, "concat synchronize");
+  }
+  return MQ_OK;
+}
+
 void mq_qtensor_free(mq_qtensor *w) {
   if (!w) return;
   if (w->data && !w->in_arena) {

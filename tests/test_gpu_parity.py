@@ -603,6 +603,39 @@ def test_from_device_blocks_at_any_alignment(dev, torch, t):
         assert _bits_equal(qt.dequantize().cpu().numpy(), ref.dequantize().cpu().numpy()), shift
 
 
+@pytest.mark.parametrize("t", TYPES + [GgmlDType.F32, GgmlDType.BF16], ids=IDS + ["F32", "BF16"])
+def test_concat_rows_is_the_row_concatenation(dev, torch, t):
+    """mq_qtensor_concat_rows: the parts' GGUF bytes in order (row counts that end
+    inside a 64-row tile and a part below one tile), dequantizing to the stacked
+    dequantized parts; parts of another type or k are refused."""
+    from mold_amd._lib import MQ_E_INVALID
+    bs = O.block_size(int(t)) if int(t) in O.WEIGHT_TYPES else 32
+    k = 2 * max(bs, 32)
+    rows = [65, 3, 128, 1]
+    _say(f"concat_rows {t.name} {rows} x {k}")
+    rng = np.random.default_rng(17)
+    blocks, parts = [], []
+    for i, n in enumerate(rows):
+        if int(t) in O.WEIGHT_TYPES:
+            b = _random_blocks(int(t), n, k, 40 + i).reshape(-1)
+        else:
+            b = rng.standard_normal(n * k).astype(np.float32)
+            b = (b if t == GgmlDType.F32 else torch.from_numpy(b).to(torch.bfloat16).view(torch.uint8).numpy())
+            b = np.ascontiguousarray(b).view(np.uint8).reshape(-1)
+        blocks.append(b)
+        parts.append(QTensor.from_blocks(dev, t, (n, k), b))
+    st = QTensor.concat_rows(dev, parts)
+    assert st.dtype() == t and st.shape == (sum(rows), k)
+    assert np.array_equal(st.data(), np.concatenate(blocks))
+    dq = torch.cat([p.dequantize() for p in parts])
+    assert _bits_equal(st.dequantize().cpu().numpy(), dq.cpu().numpy())
+    other = GgmlDType.Q8_0 if t != GgmlDType.Q8_0 else GgmlDType.Q4_0
+    odd = QTensor.from_blocks(dev, other, (1, k), np.zeros(O.row_bytes(int(other), k), np.uint8))
+    with pytest.raises(MoldqError) as e:
+        QTensor.concat_rows(dev, [parts[0], odd])
+    assert e.value.code == MQ_E_INVALID
+
+
 @pytest.mark.parametrize("t", [GgmlDType.Q4_K, GgmlDType.Q8_0], ids=lambda t: t.name)
 def test_large_host_upload_through_the_pipeline(dev, t):
     """Weights above one pinned chunk go through the threaded upload pipeline:
