@@ -651,14 +651,31 @@ static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, i
 
 // Rows per block tile.  256-row tiles decode each weight once per 256 rows of
 // x; for small m most of such a tile is padding, so up to 128 rows the tile
-// shrinks to 64 or 128 rows (more tiles, three or four workgroups per CU) and
-// from 129 to 256 rows to 128.  Up to 128 rows the launch is latency-bound:
+// shrinks to 64 or 128 rows (more tiles, three or four workgroups per CU),
+// from 129 to 256 rows to 128, and above 256 rows to 128 for some launches of
+// one partial round (below).  Up to 128 rows the launch is latency-bound:
 // its time follows the K units each workgroup walks after the tail split
 // (measured on the T5 / FLUX / Qwen shapes at m = 77 and 128: 0.71-0.85 of the
 // 256-row time), so the candidate with fewer units per workgroup wins, 64
 // rows on a tie.
 int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus) {
-  if (m > 256) return 256;
+  if (m > 256) {
+    // One partial round of 256-row tiles (few row panels, e.g. the T5 encoder
+    // and the DiT text streams at m = 512): 128-row tiles, three workgroups
+    // per CU, fill more of the chip.  They win when the 256-row tiles are few
+    // (at most a quarter of the CUs) and K short, or when the 256-row tiles must
+    // split K while the 128-row ones need not (no partial sums to write and
+    // add); elsewhere the 256 x 256 tile's efficiency wins (measured A/B:
+    // 4096 -> 4096 at m = 512 / 768 / 1024 / 2048 +14 / +5 / +2 / +12 %,
+    // 3072 -> 3072 at m = 768 +9 %; T5 up / down and FLUX text qkv at m = 512
+    // 2-7 % slower with 128 rows, every large shape 3-18 % slower).
+    const int64_t t256 = ((m + 255) / 256) * ((n + gemm_tile_n(256) - 1) / gemm_tile_n(256));
+    if (t256 >= (int64_t)cus * gemm_wgs_per_cu(256)) return 256;
+    const int64_t kp256 = tail_kparts(type, m, n, k, cus, 256, nullptr);
+    const int64_t kp128 = tail_kparts(type, m, n, k, cus, 128, nullptr);
+    if ((t256 <= cus / 4 && k <= 4096) || (kp256 >= 2 && kp128 == 1)) return 128;
+    return 256;
+  }
   if (m > 128) return 128;
   const int64_t units = k / gemm_unit_k(type);
   int best = 64;

@@ -349,13 +349,15 @@ def test_gemm_matches_f64_oracle(dev, torch, t, mnk):
 
 
 @pytest.mark.parametrize("t", TYPES, ids=IDS)
-@pytest.mark.parametrize("m", [9, 63, 64, 65, 77, 128, 129, 256, 512])
+@pytest.mark.parametrize("m", [9, 63, 64, 65, 77, 128, 129, 256, 257, 512, 768, 2048])
 def test_gemm_row_tiles_64_128_256(dev, torch, t, m):
-    """The fast GEMM's 64-, 128- and 256-row block tiles, chosen by m (64 up to 64 rows,
-    128 up to 128, 256 above), at and around each boundary: rel-L2 to f64, rows past m
-    untouched (the output is a view into a larger buffer), bf16 output, and the gated
-    epilogue; n = 4096 at k = 1024 leaves few tiles, so the partial last round also
-    takes the K split."""
+    """The fast GEMM's 64-, 128- and 256-row block tiles, chosen by m (64 or 128 up to 128
+    rows, 128 up to 256, above that 256, or 128 for a launch of one partial round of
+    256-row tiles: few tiles at short K (m = 257, 512, 768 here), or a K split that
+    128-row tiles avoid (m = 2048)), at and around each boundary: rel-L2 to f64, rows
+    past m untouched (the output is a view into a larger buffer), bf16 output, and the
+    gated epilogue; n = 4096 at k = 1024 leaves few tiles, so the partial last round
+    also takes the K split."""
     n, k = 4096, 1024
     _say(f"gemm row tiles {t.name} m={m}")
     blocks = _weights(int(t), n, k, seed=3 * m + 1)
