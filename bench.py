@@ -600,14 +600,40 @@ def bench_gemv(dev, args):
                         "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                         "frac": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                         "of_read_ceiling": round(ceil["us"] / (ms * 1e3), 4)})
-            log(f"  m={m} n={n}: {ms*1e3:.2f} us  {out[-1]['gbs']:.0f} GB/s")
             del graph
+            # the same launches on x quantized once beforehand (mq_quantize_x_q8k): the
+            # caller's producer of x (silu(vec) for every modulation of a step) does it once
+            xq = mold_amd.Q8KActivations(dev, x)
+
+            def run_q():
+                for mm in mms:
+                    mm.forward(xq, out=y)
+            run_q()
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run_q()
+            graph.replay()
+            torch.cuda.synchronize()
+            _, msq = timed(graph.replay, iters, 2, prewarm_s=0.1)
+            msq /= copies
+            del graph
+            _, msx = timed(lambda: mold_amd.Q8KActivations(dev, x), 200, 10)
+            nq = wbytes + m * (k // 256) * 304 + 4 * m * n
+            out[-1]["x_q8k"] = {"us": round(msq * 1e3, 3), "bytes": nq,
+                                "frac": round(nq / (msq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                                "of_read_ceiling": round(ceil["us"] / (msq * 1e3), 4),
+                                "quantize_us": round(msx * 1e3, 2)}
+            log(f"  m={m} n={n}: {ms*1e3:.2f} us  {out[-1]['gbs']:.0f} GB/s; x pre-quantized {msq*1e3:.2f} us "
+                f"(quantize {msx*1e3:.2f} us, once per x)")
         del mms, qts
         torch.cuda.empty_cache()
     return {"launches": out, "read_ceiling": ceilings,
             "what": "single Q4_K GEMV launches (f32 x, f32 y) replayed from a HIP graph over distinct weight "
                     "copies (> 256 MB, so reads come from HBM); read_ceiling: one streaming-read launch of the "
-                    "same weight bytes in the same run; of_read_ceiling = ceiling time / GEMV time"}
+                    "same weight bytes in the same run; of_read_ceiling = ceiling time / GEMV time; x_q8k: the "
+                    "same launches on x quantized once beforehand by mq_quantize_x_q8k (bit-identical outputs; "
+                    "quantize_us is that one kernel, timed alone with the host call)"}
 
 
 def bench_stack(stack, ms_list, args):

@@ -58,6 +58,12 @@ enum {
     MQ_E_IO = -5            /* file read / format error (GGUF) */
 };
 
+/* Activation format of mq_quantize_x_q8k (not a GGUF type): per row of x,
+ * k / 256 blocks of 304 bytes: 256 int8 quants, 8 int32 sums of 32 quants,
+ * the f32 scale d, 12 zero bytes; rows contiguous. */
+#define MQ_X_Q8K 100
+#define MQ_X_Q8K_BLOCK_BYTES 304
+
 /* Epilogue applied to x.W^T + bias before the store. */
 typedef enum mq_act { MQ_ACT_NONE = 0, MQ_ACT_GELU_TANH = 1 } mq_act;
 
@@ -178,7 +184,11 @@ int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, vo
  * f32 [n] or NULL.  Picks the skinny GEMV for small m and the fused
  * dequant-MFMA GEMM otherwise.  Replaces QCudaStorage::fwd, reached from
  * crates/mold-inference/src/flux2/quantized_transformer.rs:40-45 and the FLUX
- * quantized model's linears. */
+ * quantized model's linears.  For a Q4_K weight at m <= 8, x may also be
+ * given as mq_quantize_x_q8k's blocks (x_dtype MQ_X_Q8K, ldx = k, 16-byte
+ * aligned): the same result bit for bit as the F32 / BF16 x they came from,
+ * without re-quantizing x in every call (MQ_E_UNSUPPORTED for other weights
+ * or m, and for the gated call). */
 int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
                int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
                const float *bias, int act, void *stream);
@@ -230,6 +240,19 @@ int mq_qk_norm_rope(const void *qkv, int qkv_dtype, int64_t ld, int64_t rows, in
                     const void *q_weight, const void *k_weight, float eps, const float *cos_table,
                     const float *sin_table, void *q_out, void *k_out, void *v_out, int64_t row_off, int64_t l_total,
                     void *stream);
+
+/* Quantize activations once for several Q4_K GEMVs: x [m, k] (F32 or BF16,
+ * row stride ldx, 16-byte aligned rows) -> m * k / 256 blocks of
+ * MQ_X_Q8K_BLOCK_BYTES at dst (16-byte aligned), by the Q8_K quantization
+ * mq_qmatmul's Q4_K GEMV applies to x (candle's BlockQ8K::from_float
+ * convention: iscale = -128 / the first value of largest magnitude, round
+ * half away from zero, clamp at 127).  No candle counterpart: candle's CUDA
+ * path re-quantizes x (to Q8_1) in every QMatMul::forward; mold's
+ * modulation linears of one step all read the same silu(vec)
+ * (crates/mold-inference/src/flux/offload.rs:143-156).  Asynchronous on
+ * stream. */
+int mq_quantize_x_q8k(mq_ctx *ctx, const void *x, int x_dtype, int64_t m, int64_t k, int64_t ldx, void *dst,
+                      void *stream);
 
 /* The DiT blocks' gated residual update through one quantized linear:
  * y[m, :n] += gate[:n] * (x[m, :k] . W^T + bias), y f32 (row stride ldy),

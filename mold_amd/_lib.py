@@ -12,6 +12,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoldq.so")
 
 MQ_OK, MQ_E_INVALID, MQ_E_HIP, MQ_E_OOM, MQ_E_UNSUPPORTED, MQ_E_IO = 0, -1, -2, -3, -4, -5
+MQ_X_Q8K, MQ_X_Q8K_BLOCK_BYTES = 100, 304   # mq_quantize_x_q8k's activation blocks
 
 # Every symbol include/moldq.h declares, with (restype, argtypes).
 _vp, _i64, _int, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
@@ -40,6 +41,7 @@ SIGNATURES = {
                                ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "mq_dequantize": (_int, [_vp, _vp, _vp, _int, _vp]),
     "mq_qmatmul": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _int, _i64, _vp, _int, _vp]),
+    "mq_quantize_x_q8k": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
     "mq_qmatmul_noalloc": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _int, _i64, _vp, _int, _vp]),
     "mq_qmatmul_gated_add": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     "mq_adaln_modulate": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, ctypes.c_float, _vp, _i64, _vp]),

@@ -283,7 +283,15 @@ int check_qmatmul_args(const char *fn, const mq_ctx *ctx, const mq_qtensor *w, c
                 "%s: the weight is a dense %s tensor; like candle's QMatMul::from_arc, dequantize it once "
                 "(mq_dequantize) and use the device's dense matmul",
                 fn, dense_name(w->dtype));
-  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: x dtype %d must be F32 or BF16", fn, x_dtype);
+  if (x_dtype == MQ_X_Q8K) {
+    if (!gemv_takes_x_q8k(w->dtype, m, w->n, w->k, ctx->cu_count))
+      return fail(MQ_E_UNSUPPORTED, "%s: x in MQ_X_Q8K form needs a Q4_K weight, m <= %d and the GEMV's shape limits", fn,
+                  kGemvMaxM);
+    if (ldx != w->k || (reinterpret_cast<uintptr_t>(x) & 15) != 0)
+      return fail(MQ_E_INVALID, "%s: MQ_X_Q8K x must be contiguous rows (ldx = k) at a 16-byte aligned address", fn);
+  } else if (x_dtype != MQ_F32 && x_dtype != MQ_BF16) {
+    return fail(MQ_E_INVALID, "%s: x dtype %d must be F32, BF16 or MQ_X_Q8K", fn, x_dtype);
+  }
   if (y_dtype != MQ_F32 && y_dtype != MQ_BF16) return fail(MQ_E_INVALID, "%s: y dtype %d must be F32 or BF16", fn, y_dtype);
   if (ldx < w->k) return fail(MQ_E_INVALID, "%s: ldx=%lld < k=%lld", fn, (long long)ldx, (long long)w->k);
   if (ldy < w->n) return fail(MQ_E_INVALID, "%s: ldy=%lld < n=%lld", fn, (long long)ldy, (long long)w->n);
@@ -796,8 +804,14 @@ int mq_dequantize(mq_ctx *ctx, const mq_qtensor *w, void *dst, int dst_dtype, vo
 int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int64_t m, int gated, size_t *bytes) {
   if (!ctx || !w || !bytes) return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: NULL argument");
   if (m < 0) return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: m=%lld < 0", (long long)m);
-  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
-    return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: x dtype %d must be F32 or BF16", x_dtype);
+  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16 && x_dtype != MQ_X_Q8K)
+    return fail(MQ_E_INVALID, "mq_qmatmul_workspace_size: x dtype %d must be F32, BF16 or MQ_X_Q8K", x_dtype);
+  if (x_dtype == MQ_X_Q8K) {  // the GEMV reads it in place: no scratch
+    if (!gemv_takes_x_q8k(w->dtype, m, w->n, w->k, ctx->cu_count) || gated)
+      return fail(MQ_E_UNSUPPORTED, "mq_qmatmul_workspace_size: no MQ_X_Q8K GEMV for this weight and m");
+    *bytes = 0;
+    return MQ_OK;
+  }
   if (is_dense(w->dtype))
     return fail(MQ_E_UNSUPPORTED, "mq_qmatmul_workspace_size: dense %s weights take no quantized matmul",
                 dense_name(w->dtype));
@@ -823,6 +837,24 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
   return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
 }
 
+int mq_quantize_x_q8k(mq_ctx *ctx, const void *x, int x_dtype, int64_t m, int64_t k, int64_t ldx, void *dst,
+                      void *stream) {
+  if (!ctx || ((!x || !dst) && m > 0)) return fail(MQ_E_INVALID, "mq_quantize_x_q8k: NULL argument");
+  if (m < 0 || k <= 0 || k % 256 != 0 || ldx < k)
+    return fail(MQ_E_INVALID, "mq_quantize_x_q8k: m=%lld, k=%lld (a multiple of 256), ldx=%lld", (long long)m,
+                (long long)k, (long long)ldx);
+  if (x_dtype != MQ_F32 && x_dtype != MQ_BF16)
+    return fail(MQ_E_INVALID, "mq_quantize_x_q8k: x dtype %d must be F32 or BF16", x_dtype);
+  const int64_t es = x_dtype == MQ_F32 ? 4 : 2;
+  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(dst)) & 15) != 0 || (ldx * es) % 16 != 0)
+    return fail(MQ_E_INVALID, "mq_quantize_x_q8k: x rows and dst must be 16-byte aligned");
+  if (m == 0) return MQ_OK;
+  DeviceGuard g(ctx->device);
+  const hipError_t e = launch_quantize_x_q8k(x, x_dtype, m, k, ldx, dst, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "quantize x to Q8_K");
+  return MQ_OK;
+}
+
 int mq_qmatmul_noalloc(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
                        int y_dtype, int64_t ldy, const float *bias, int act, void *stream) {
   int rc = check_qmatmul_args("mq_qmatmul_noalloc", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
@@ -844,6 +876,7 @@ int mq_qmatmul_noalloc(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dt
 
 int mq_qmatmul_gated_add(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx,
                          float *y, int64_t ldy, const float *bias, const float *gate, void *stream) {
+  if (x_dtype == MQ_X_Q8K) return fail(MQ_E_UNSUPPORTED, "mq_qmatmul_gated_add: x in MQ_X_Q8K form takes the GEMV only");
   int rc = check_qmatmul_args("mq_qmatmul_gated_add", ctx, w, x, x_dtype, m, ldx, y, MQ_F32, ldy, MQ_ACT_NONE);
   if (rc || m == 0) return rc;
   if (!gate) return fail(MQ_E_INVALID, "mq_qmatmul_gated_add: NULL gate");

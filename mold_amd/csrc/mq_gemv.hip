@@ -168,9 +168,52 @@ __device__ __forceinline__ int row16_min(int v) {
 
 // LDS of the Q4_K GEMV: x as given (f32 or bf16, 256 elements per
 // super-block and row of x), its Q8_K form (256 quants, 8 sub-block sums and
-// d), then one f32 partial per (super-block, row, m).
+// d), then one f32 partial per (super-block, row, m).  For x given already in
+// Q8_K form (MQ_X_Q8K) the blocks are copied in as they are, kQ8kXBytes each.
 __host__ __device__ inline size_t q4k_lds_bytes(int64_t nb, int m, int64_t rows, int xsize) {
-  return (size_t)nb * m * (256 * xsize + 256 + 32 + 4) + (size_t)nb * rows * m * 4;
+  return (size_t)nb * m * (xsize < 0 ? kQ8kXBytes : 256 * xsize + 256 + 32 + 4) + (size_t)nb * rows * m * 4;
+}
+
+// One item (256 elements of one row of x) to Q8_K, held by a 16-lane group:
+// lane l16 holds elements 16 l16 .. 16 l16 + 15 in v.  iscale = -128 / (the
+// first element of largest magnitude), q = min(round_half_away(iscale x),
+// 127), d = 1 / iscale (all zero for an all-zero item).  Returns the lane's 16
+// quants packed, and in qsum the sum of its sub-block's 32 quants (lanes l16
+// and l16 ^ 1 hold one sub-block).
+__device__ __forceinline__ float q8k_quantize16(const float v[16], int l16, int lane, uint32_t packed[4], int &qsum) {
+  // largest magnitude over the item, then the value of its first occurrence
+  // in element order: the lowest element index holding it, taken from the
+  // lane that owns that index (with no hit, as for an all-NaN item, element 3)
+  float lmax = __builtin_fabsf(v[0]);
+#pragma unroll
+  for (int i = 1; i < 16; ++i) lmax = __builtin_fmaxf(lmax, __builtin_fabsf(v[i]));
+  const float amax = row16_max(lmax);
+  int first = 16;
+  float cand = v[3];
+#pragma unroll
+  for (int i = 15; i >= 0; --i) {
+    const bool hit = __builtin_fabsf(v[i]) == amax;
+    first = hit ? i : first;
+    cand = hit ? v[i] : cand;
+  }
+  const int gfirst = row16_min(first < 16 ? 16 * l16 + first : 256);
+  const int src = (lane & ~15) + (gfirst < 256 ? gfirst >> 4 : 0);
+  const float vmax = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(cand)));
+  packed[0] = packed[1] = packed[2] = packed[3] = 0u;
+  qsum = 0;
+  float dx = 0.f;
+  if (amax != 0.f) {
+    const float iscale = -128.f / vmax;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = (int)__builtin_fminf(__builtin_roundf(iscale * v[i]), 127.f);
+      qsum += q;
+      packed[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+    }
+    dx = 1.f / iscale;
+  }
+  qsum += dpp<0xB1, 0xF>(qsum);  // the sub-block's other half (lane L ^ 1)
+  return dx;
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -194,13 +237,29 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     WView w, int64_t n, int64_t nrows_mem, int nb, int rows, const XT *__restrict__ x, int64_t ldx,
     OUT *__restrict__ y, int64_t ldy, const float *__restrict__ bias, int act) {
   extern __shared__ __align__(16) uint8_t smem[];
-  constexpr int kXs = (int)sizeof(XT);
+  // x given in Q8_K form (MQ_X_Q8K): its blocks are copied into LDS as they are
+  constexpr bool kQ8 = __is_same(XT, Q8kX);
+  constexpr int kXs = kQ8 ? 0 : (int)sizeof(XT);
   const XT *xl = reinterpret_cast<const XT *>(smem);                          // [nb][M][256] x
   uint8_t *q8 = smem + (size_t)nb * M * 256 * kXs;
   uint32_t *xq = reinterpret_cast<uint32_t *>(q8);                            // [nb][M][64] packed i8
   int32_t *xs = reinterpret_cast<int32_t *>(q8 + (size_t)nb * M * 256);       // [nb][M][8]
   float *xd = reinterpret_cast<float *>(q8 + (size_t)nb * M * 288);           // [nb][M]
-  float *red = reinterpret_cast<float *>(q8 + (size_t)nb * M * 292);          // [nb * rows][M]
+  float *red = reinterpret_cast<float *>(q8 + (size_t)nb * M * (kQ8 ? kQ8kXBytes : 292));  // [nb * rows][M]
+  // item (super-block sb, row m of x): its 64 packed quant words, 8 sub-block
+  // sums and d (kQ8: block m * nb + sb of the copied rows)
+  auto x_words = [&](int sb, int m) -> const uint32_t * {
+    if constexpr (kQ8) return reinterpret_cast<const uint32_t *>(q8 + (size_t)(m * nb + sb) * kQ8kXBytes);
+    else return xq + (sb * M + m) * 64;
+  };
+  auto x_sums = [&](int sb, int m) -> const int32_t * {
+    if constexpr (kQ8) return reinterpret_cast<const int32_t *>(q8 + (size_t)(m * nb + sb) * kQ8kXBytes + 256);
+    else return xs + (sb * M + m) * 8;
+  };
+  auto x_d = [&](int sb, int m) -> float {
+    if constexpr (kQ8) return *reinterpret_cast<const float *>(q8 + (size_t)(m * nb + sb) * kQ8kXBytes + 288);
+    else return xd[sb * M + m];
+  };
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int64_t r0 = (int64_t)blockIdx.x * rows;
@@ -234,7 +293,22 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
   //    every load is unconditional).
   const int nitems = nb * M;
   constexpr int kWaves = kQ4kThreads / 64;
-  {
+  Q4kPair slot[kOne ? 1 : 2];
+  if constexpr (kQ8) {
+    // x's blocks (M rows of nb, contiguous) into LDS as they are, 1 KiB per
+    // wave load (lanes past the end issue nothing), then at once the first
+    // pair's weights: x, a few KiB that every workgroup reads, comes from L2
+    // and is not queued behind them.  The wait leaves at most the pair's
+    // weight loads in flight (10 or more vector loads, issued after x).
+    const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t *)smem;
+    const int xbytes = nitems * kQ8kXBytes;
+    const uint8_t *xb = reinterpret_cast<const uint8_t *>(x);
+    for (int c = wave; c * 1024 < xbytes; c += kWaves)
+      if (c * 1024 + 16 * lane < xbytes) dma16(xb + c * 1024 + 16 * lane, lbase + (uint32_t)(c * 1024));
+    load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
+    asm volatile("s_waitcnt vmcnt(10)" ::: "memory");  // this wave's x
+    __syncthreads();
+  } else {
     const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t *)smem;
     if constexpr (kXs == 4) {
       for (int j = wave; j < nitems; j += kWaves) {
@@ -252,10 +326,11 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
       }
     }
   }
-  Q4kPair slot[kOne ? 1 : 2];
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's x
-  __syncthreads();
-  load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
+  if constexpr (!kQ8) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's x
+    __syncthreads();
+    load_pair(tid < npairs ? tid : npairs - 1, slot[0]);
+  }
 
   // 2. Q8_K staging: one item per 16-lane group (32 groups, every one at
   //    once); lane L of a group holds elements 16L..16L+15, half of sub-block
@@ -285,44 +360,17 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
         }
       }
     }
-    // largest magnitude over the item, then the value of its first occurrence
-    // in element order: the lowest element index holding it, taken from the
-    // lane that owns that index (with no hit, as for an all-NaN item, element 3)
-    float lmax = __builtin_fabsf(v[0]);
-#pragma unroll
-    for (int i = 1; i < 16; ++i) lmax = __builtin_fmaxf(lmax, __builtin_fabsf(v[i]));
-    const float amax = row16_max(lmax);
-    int first = 16;
-    float cand = v[3];
-#pragma unroll
-    for (int i = 15; i >= 0; --i) {
-      const bool hit = __builtin_fabsf(v[i]) == amax;
-      first = hit ? i : first;
-      cand = hit ? v[i] : cand;
-    }
-    const int gfirst = row16_min(first < 16 ? 16 * l16 + first : 256);
-    const int src = (tid & 63 & ~15) + (gfirst < 256 ? gfirst >> 4 : 0);
-    const float vmax = __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(cand)));
-    uint32_t packed[4] = {0u, 0u, 0u, 0u};
-    int qsum = 0;
-    float dx = 0.f;
-    if (amax != 0.f) {
-      const float iscale = -128.f / vmax;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int q = (int)__builtin_fminf(__builtin_roundf(iscale * v[i]), 127.f);
-        qsum += q;
-        packed[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
-      }
-      dx = 1.f / iscale;
-    }
+    uint32_t packed[4];
+    int qsum;
+    const float dx = q8k_quantize16(v, l16, tid & 63, packed, qsum);
     *reinterpret_cast<uint4 *>(xq + j * 64 + 4 * l16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    qsum += dpp<0xB1, 0xF>(qsum);  // the sub-block's other half (lane L ^ 1)
     if ((l16 & 1) == 0) xs[j * 8 + (l16 >> 1)] = qsum;
     if (l16 == 0) xd[j] = dx;
   };
-  for (int j = g16; j < nitems; j += kQ4kThreads / 16) stage(j);
-  __syncthreads();
+  if constexpr (!kQ8) {
+    for (int j = g16; j < nitems; j += kQ4kThreads / 16) stage(j);
+    __syncthreads();
+  }
 
   // 3. per pair: integer dot against Q8_K x, one f32 partial per m
   auto dot_pair = [&](int p, const Q4kPair &cur) {
@@ -350,7 +398,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
       // sdot4 chain of 8 per sub-block and row m of x.  The 64 Q8_K bytes of
       // step s + 1 are read from LDS while step s computes (two register slots).
       auto xload = [&](int g, int m, uint4 *dst) {
-        const uint4 *xb = reinterpret_cast<const uint4 *>(xq + (sb * M + m) * 64 + 16 * g);
+        const uint4 *xb = reinterpret_cast<const uint4 *>(x_words(sb, m) + 16 * g);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = xb[i];
       };
@@ -400,7 +448,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
         }
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const uint32_t *xb = xq + (sb * M + m) * 64 + 16 * g;
+          const uint32_t *xb = x_words(sb, m) + 16 * g;
           const uint4 x0 = *reinterpret_cast<const uint4 *>(xb);
           const uint4 x1 = *reinterpret_cast<const uint4 *>(xb + 4);
           const uint4 x2 = *reinterpret_cast<const uint4 *>(xb + 8);
@@ -421,14 +469,13 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     const float d = h2f((uint16_t)(cur.dm & 0xFFFF)), dmin = h2f((uint16_t)(cur.dm >> 16));
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      const int j = sb * M + m;
-      const int4 ba = *reinterpret_cast<const int4 *>(xs + j * 8);
-      const int4 bb = *reinterpret_cast<const int4 *>(xs + j * 8 + 4);
+      const int4 ba = *reinterpret_cast<const int4 *>(x_sums(sb, m));
+      const int4 bb = *reinterpret_cast<const int4 *>(x_sums(sb, m) + 4);
       const int smin = __mul24((int)(m03 & 0xFF), ba.x) + __mul24((int)((m03 >> 8) & 0xFF), ba.y) +
                        __mul24((int)((m03 >> 16) & 0xFF), ba.z) + __mul24((int)(m03 >> 24), ba.w) +
                        __mul24((int)(m47 & 0xFF), bb.x) + __mul24((int)((m47 >> 8) & 0xFF), bb.y) +
                        __mul24((int)((m47 >> 16) & 0xFF), bb.z) + __mul24((int)(m47 >> 24), bb.w);
-      const float dx = xd[j];
+      const float dx = x_d(sb, m);
       if (valid) red[p * M + m] = __builtin_fmaf(d * dx, (float)S[m], -(dmin * dx) * (float)smin);
     }
   };
@@ -670,7 +717,7 @@ static void launch_gemv_q4k(const WView &w, int64_t n, int64_t k, const XT *x, i
   const bool one = q4k_one_slot(nb, rows);
   const int64_t wgs = (n + rows - 1) / rows;
   const int64_t nrows_mem = ((n + kRowTile - 1) / kRowTile) * kRowTile;
-  const size_t lds = q4k_lds_bytes(nb, M, rows, (int)sizeof(XT));
+  const size_t lds = q4k_lds_bytes(nb, M, rows, __is_same(XT, Q8kX) ? -1 : (int)sizeof(XT));
   if (one)
     hipLaunchKernelGGL((gemv_q4k_kernel<M, XT, OUT, true>), dim3((unsigned)wgs), dim3(kQ4kThreads), lds, stream, w,
                        n, nrows_mem, (int)nb, rows, x, ldx, y, ldy, bias, act);
@@ -726,6 +773,67 @@ static void launch_gemv_q4k_m(const WView &w, int64_t n, int64_t k, const XT *x,
   }
 }
 
+// x -> MQ_X_Q8K blocks: one 256-element item (row, super-block) per 16-lane
+// group, 32 per workgroup, by the Q4_K GEMV's own quantization of its staged
+// x (q8k_quantize16), so a GEMV on the blocks equals one on x bit for bit.
+template <typename XT>
+__global__ __launch_bounds__(512) void quantize_x_q8k_kernel(const XT *__restrict__ x, int64_t m, int64_t nb,
+                                                             int64_t ldx, uint8_t *__restrict__ dst) {
+  const int tid = threadIdx.x, l16 = tid & 15;
+  const int64_t items = m * nb;
+  const int64_t j0 = (int64_t)blockIdx.x * 32 + (tid >> 4);
+  const bool valid = j0 < items;
+  const int64_t j = valid ? j0 : items - 1;  // every lane joins the group's cross-lane steps
+  const int64_t row = j / nb, sb = j - row * nb;
+  const XT *src = x + row * ldx + sb * 256 + 16 * l16;
+  float v[16];
+  if constexpr (__is_same(XT, float)) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 t = reinterpret_cast<const float4 *>(src)[c];
+      v[4 * c] = t.x;
+      v[4 * c + 1] = t.y;
+      v[4 * c + 2] = t.z;
+      v[4 * c + 3] = t.w;
+    }
+  } else {
+    // bf16 -> f32 is exact: the 16 bits become the high half
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const uint4 t = reinterpret_cast<const uint4 *>(src)[c];
+      const uint32_t wd[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[8 * c + 2 * i] = __uint_as_float(wd[i] << 16);
+        v[8 * c + 2 * i + 1] = __uint_as_float(wd[i] & 0xFFFF0000u);
+      }
+    }
+  }
+  uint32_t packed[4];
+  int qsum;
+  const float d = q8k_quantize16(v, l16, tid & 63, packed, qsum);
+  if (!valid) return;
+  uint8_t *blk = dst + j * kQ8kXBytes;
+  *reinterpret_cast<uint4 *>(blk + 16 * l16) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  if ((l16 & 1) == 0) *reinterpret_cast<int32_t *>(blk + 256 + 2 * l16) = qsum;
+  if (l16 == 0) *reinterpret_cast<float *>(blk + 288) = d;
+  if (l16 >= 1 && l16 <= 3) *reinterpret_cast<uint32_t *>(blk + 288 + 4 * l16) = 0u;  // the 12 pad bytes
+}
+
+hipError_t launch_quantize_x_q8k(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, void *dst,
+                                 hipStream_t stream) {
+  const int64_t nb = k / 256, items = m * nb;
+  if (items <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((items + 31) / 32);
+  if (x_type == F32)
+    hipLaunchKernelGGL((quantize_x_q8k_kernel<float>), dim3(grid), dim3(512), 0, stream,
+                       static_cast<const float *>(x), m, nb, ldx, static_cast<uint8_t *>(dst));
+  else
+    hipLaunchKernelGGL((quantize_x_q8k_kernel<__bf16>), dim3(grid), dim3(512), 0, stream,
+                       static_cast<const __bf16 *>(x), m, nb, ldx, static_cast<uint8_t *>(dst));
+  return hipGetLastError();
+}
+
 template <int TYPE, typename OUT>
 static void launch_gemv_m(const WView &w, int64_t n, int64_t k, const float *x, int64_t m, int64_t ldx,
                           OUT *y, int64_t ldy, const float *bias, int act, float *partial, hipStream_t stream) {
@@ -749,14 +857,27 @@ static bool q4k_x_aligned(const void *x, int x_type, int64_t ldx) {
 
 bool gemv_reads_x_in_place(int type, int64_t m, int64_t n, int64_t k, const void *x, int x_type, int64_t ldx,
                            int cus) {
+  if (x_type == MQ_X_Q8K) return gemv_takes_x_q8k(type, m, n, k, cus);
   return type == Q4_K && m >= 1 && m <= kGemvMaxM && q4k_rows(n, k / 256, m, cus) > 0 &&
          q4k_x_aligned(x, x_type, ldx);
+}
+
+bool gemv_takes_x_q8k(int type, int64_t m, int64_t n, int64_t k, int cus) {
+  return type == Q4_K && m >= 1 && m <= kGemvMaxM && k % 256 == 0 && q4k_rows(n, k / 256, m, cus) > 0;
 }
 
 hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const void *x, int x_type, int64_t m,
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
                        float *partial, int cus, hipStream_t stream) {
   if (m <= 0 || n <= 0) return hipSuccess;
+  if (x_type == MQ_X_Q8K) {  // the caller checked: Q4_K, m <= 8, q4k rows, aligned contiguous blocks
+    const Q8kX *xq = static_cast<const Q8kX *>(x);
+    if (y_type == F32)
+      launch_gemv_q4k_m<Q8kX, float>(w, n, k, xq, m, ldx, static_cast<float *>(y), ldy, bias, act, cus, stream);
+    else
+      launch_gemv_q4k_m<Q8kX, __bf16>(w, n, k, xq, m, ldx, static_cast<__bf16 *>(y), ldy, bias, act, cus, stream);
+    return hipGetLastError();
+  }
   if (gemv_reads_x_in_place(type, m, n, k, x, x_type, ldx, cus)) {
     if (x_type == F32) {
       if (y_type == F32)

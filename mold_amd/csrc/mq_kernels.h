@@ -1,6 +1,7 @@
 // mq_kernels.h — launchers shared between the kernel files and the C ABI.
 #pragma once
 
+#include "../../include/moldq.h"
 #include "mq_common.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -41,6 +42,18 @@ constexpr int kGemvMaxM = 8;
 bool gemv_reads_x_in_place(int type, int64_t m, int64_t n, int64_t k, const void *x, int x_type, int64_t ldx,
                            int cus);
 size_t gemv_scratch_bytes(int type, int64_t m, int64_t n, int64_t k, int cus);
+// x pre-quantized for the Q4_K GEMV (MQ_X_Q8K): per row, k / 256 blocks of
+// kQ8kXBytes (256 int8 quants, 8 int32 sums of 32 quants, f32 d, 12 zero bytes).
+constexpr int kQ8kXBytes = MQ_X_Q8K_BLOCK_BYTES;
+struct Q8kX {
+  uint8_t b[kQ8kXBytes];
+};
+// x [m, k] (f32 or bf16, row stride ldx) -> m * k / 256 blocks at dst, by the
+// same Q8_K quantization the Q4_K GEMV applies to x when it stages it.
+// Whether mq_qmatmul's GEMV takes x in MQ_X_Q8K form for this weight and m.
+bool gemv_takes_x_q8k(int type, int64_t m, int64_t n, int64_t k, int cus);
+hipError_t launch_quantize_x_q8k(const void *x, int x_type, int64_t m, int64_t k, int64_t ldx, void *dst,
+                                 hipStream_t stream);
 hipError_t launch_gemv(int type, const WView &w, int64_t n, int64_t k, const void *x, int x_type, int64_t m,
                        int64_t ldx, void *y, int y_type, int64_t ldy, const float *bias, int act,
                        float *partial, int cus, hipStream_t stream);

@@ -247,6 +247,20 @@ class QMatMul:
     def forward(self, x, bias=None, act: int = ACT_NONE, out_dtype=None, out=None, stream=None):
         torch = _torch()
         n, k = self.w.shape
+        if isinstance(x, Q8KActivations):
+            if x.k != k:
+                raise ValueError(f"QMatMul: x k {x.k} != weight k {k}")
+            out_dtype = out_dtype or (out.dtype if out is not None else torch.float32)
+            if out is None:
+                out = torch.empty((x.m, n), dtype=out_dtype, device=x.data.device)
+            assert out.dtype == out_dtype and tuple(out.shape) == (x.m, n)
+            if bias is not None:
+                assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == n
+            check(_lib.load().mq_qmatmul(self.w.device.handle, self.w.handle, x.data.data_ptr(), _lib.MQ_X_Q8K, x.m,
+                                         k, out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
+                                         bias.data_ptr() if bias is not None else None, int(act),
+                                         _stream_ptr(stream)))
+            return out.reshape(*x.lead, n)
         if x.shape[-1] != k:
             raise ValueError(f"QMatMul: x last dim {x.shape[-1]} != weight k {k}")
         lead = x.shape[:-1]
@@ -268,6 +282,26 @@ class QMatMul:
         return out.reshape(*lead, n)
 
     __call__ = forward
+
+
+class Q8KActivations:
+    """Activations quantized once (mq_quantize_x_q8k) for several Q4_K GEMVs
+    (m <= 8): QMatMul.forward on them equals QMatMul.forward on the f32 / bf16 x
+    they came from, bit for bit, without re-quantizing x in every call.  Every
+    adaLN modulation linear of a DiT step reads the same silu(vec)
+    (crates/mold-inference/src/flux/offload.rs:143-156)."""
+
+    def __init__(self, device: Device, x, stream=None):
+        torch = _torch()
+        x2 = x.reshape(-1, x.shape[-1])
+        if x2.stride(1) != 1 or (x2.data_ptr() % 16) or (x2.stride(0) * x2.element_size()) % 16:
+            x2 = x2.contiguous()
+        self.m, self.k = int(x2.shape[0]), int(x2.shape[1])
+        self.lead = tuple(x.shape[:-1])
+        self.data = torch.empty((self.m, (self.k // 256) * _lib.MQ_X_Q8K_BLOCK_BYTES), dtype=torch.uint8,
+                                device=x.device)
+        check(_lib.load().mq_quantize_x_q8k(device.handle, x2.data_ptr(), _dtype_code(x2.dtype), self.m, self.k,
+                                            x2.stride(0), self.data.data_ptr(), _stream_ptr(stream)))
 
 
 class Linear:

@@ -69,3 +69,26 @@ def test_lds_dma_kernels_leave_m0_alone_and_do_not_spill(tmp_path, src, defines,
     for name, (lines, meta) in funcs.items():
         assert not _m0_outside_asm(lines), (name, _m0_outside_asm(lines)[:3])
         assert meta.get("ScratchSize", 0) == 0, (name, meta)
+
+
+VMEM_LOAD = re.compile(r"^\s*(global_|buffer_|flat_)load")
+
+
+def test_gemv_pre_quantized_x_wait_covers_its_dma(tmp_path):
+    """The Q4_K GEMV on pre-quantized x issues x's LDS DMA, then its first weight loads,
+    then waits vmcnt(10) for x: every path from a DMA to that wait must issue at least
+    10 vector loads after the DMA (the first pair's 10 or more), so the wait covers it."""
+    funcs = {k: v for k, v in _functions(_asm(tmp_path, "mq_gemv.hip")).items()
+             if "gemv_q4k_kernel" in k and "Q8kX" in k}
+    assert funcs, "no gemv_q4k_kernel<.., Q8kX, ..> in the assembly"
+    for name, (lines, _) in funcs.items():
+        body = [ln.strip() for ln in lines if ln.strip() and not ln.strip().startswith(";")]
+        waits = [i for i, ln in enumerate(body) if ln.startswith("s_waitcnt vmcnt(10)")]
+        assert len(waits) == 1, (name, len(waits))
+        w = waits[0]
+        dmas = [i for i in range(w) if "global_load_lds_dwordx4" in body[i]]
+        assert dmas, name
+        loads = sum(1 for i in range(dmas[-1] + 1, w) if VMEM_LOAD.match(body[i]))
+        assert loads >= 10, (name, loads)
+        # no branch back into the DMA loop between the loads and the wait
+        assert not any(re.match(r"s_cbranch|s_branch", body[i]) for i in range(dmas[-1] + 1 + loads, w)), name

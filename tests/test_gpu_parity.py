@@ -272,6 +272,84 @@ def test_gemv_q8k_activation_edge_cases(dev, torch):
     print(f"[report] edge cases vs candle CPU restatement: rel-L2 {O.rel_l2(y, cand):.2e}", flush=True)
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("n,k", [(18432, 3072), (9216, 3072), (1000, 256), (4096, 4096)], ids=str)
+def test_gemv_q4k_pre_quantized_x_bit_identical(dev, torch, m, n, k):
+    """mq_quantize_x_q8k + mq_qmatmul(x_dtype = MQ_X_Q8K) equals mq_qmatmul on the f32 /
+    bf16 x itself bit for bit (both quantize x by the same code), with bias, GELU and a
+    bf16 output; reusing one quantized x for two weights is the same as two calls.  Where
+    the Q4_K GEMV does not run (m = 8 at K = 3072: its LDS would not hold x as f32) the
+    pre-quantized form is refused."""
+    from mold_amd._lib import MQ_E_UNSUPPORTED, MQ_X_Q8K
+    _say(f"gemv pre-quantized x m={m} [{n},{k}]")
+    g = torch.Generator(device="cuda").manual_seed(n + k + m)
+    qt = QTensor.quantize(dev, torch.randn((n, k), device="cuda", generator=g) * 0.02, GgmlDType.Q4_K)
+    size = ctypes.c_size_t()
+    if mold_amd._lib.load().mq_qmatmul_workspace_size(dev.handle, qt.handle, MQ_X_Q8K, m, 0,
+                                                       ctypes.byref(size)) == MQ_E_UNSUPPORTED:
+        assert m >= 4, (m, n, k)
+        with pytest.raises(MoldqError) as e:
+            QMatMul(qt).forward(mold_amd.Q8KActivations(dev, torch.randn((m, k), device="cuda")))
+        assert e.value.code == MQ_E_UNSUPPORTED
+        return
+    qt2 = QTensor.quantize(dev, torch.randn((n, k), device="cuda", generator=g) * 0.02, GgmlDType.Q4_K)
+    bias = torch.randn(n, device="cuda", generator=g)
+    for xdt in (torch.float32, torch.bfloat16):
+        x = (torch.randn((m, k), device="cuda", generator=g) * 3).to(xdt)
+        xq = mold_amd.Q8KActivations(dev, x)
+        for w in (qt, qt2):
+            mm = QMatMul(w)
+            assert torch.equal(mm.forward(xq, out_dtype=torch.float32), mm.forward(x, out_dtype=torch.float32))
+            a = mm.forward(xq, bias=bias, act=mold_amd.ACT_GELU_TANH, out_dtype=torch.bfloat16)
+            b = mm.forward(x, bias=bias, act=mold_amd.ACT_GELU_TANH, out_dtype=torch.bfloat16)
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    torch.cuda.synchronize()
+
+
+def test_quantize_x_q8k_blocks_match_the_oracle(dev, torch):
+    """The blocks' quants and scale are the oracle's Q8_K (candle's BlockQ8K convention as
+    restated there), the sums are its per-16 sums added in pairs, the pad bytes zero;
+    an all-zero item gives d = 0 and zero quants."""
+    from mold_amd._lib import MQ_X_Q8K_BLOCK_BYTES as B
+    m, k = 3, 1024
+    x = np.random.default_rng(12).standard_normal((m, k)).astype(np.float32) * 5
+    x[1, 256:512] = 0.0
+    x[2, 3] = -x[2, :256].__abs__().max() * 1.5       # a negative first maximum
+    xq = mold_amd.Q8KActivations(dev, torch.from_numpy(x).cuda())
+    got = xq.data.cpu().numpy().reshape(m, k // 256, B)
+    for r in range(m):
+        ref = O.quantize_act(O.Q4_K, x[r]).reshape(k // 256, 292)
+        for sb in range(k // 256):
+            d_ref = ref[sb, :4].view(np.float32)[0]
+            qs_ref = ref[sb, 4:260]
+            bs_ref = ref[sb, 260:292].view(np.int16).astype(np.int32)
+            assert np.array_equal(got[r, sb, :256], qs_ref), (r, sb)
+            assert np.array_equal(got[r, sb, 256:288].view(np.int32), bs_ref[0::2] + bs_ref[1::2]), (r, sb)
+            assert got[r, sb, 288:292].view(np.float32)[0].tobytes() == np.float32(d_ref).tobytes(), (r, sb)
+            assert not got[r, sb, 292:].any()
+    assert not got[1, 1, :288].any()
+
+
+def test_pre_quantized_x_refused_outside_the_q4k_gemv(dev, torch):
+    from mold_amd._lib import MQ_E_UNSUPPORTED, MQ_E_INVALID
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn((2, 512), device="cuda", generator=g)
+    xq = mold_amd.Q8KActivations(dev, x)
+    q8 = QTensor.quantize(dev, torch.randn((64, 512), device="cuda", generator=g), GgmlDType.Q8_0)
+    with pytest.raises(MoldqError) as e:
+        QMatMul(q8).forward(xq)
+    assert e.value.code == MQ_E_UNSUPPORTED
+    q4 = QTensor.quantize(dev, torch.randn((64, 512), device="cuda", generator=g), GgmlDType.Q4_K)
+    lib = mold_amd._lib.load()
+    res, gate = torch.zeros((2, 64), device="cuda"), torch.zeros(64, device="cuda")
+    assert lib.mq_qmatmul_gated_add(dev.handle, q4.handle, xq.data.data_ptr(), mold_amd._lib.MQ_X_Q8K, 2, 512,
+                                    res.data_ptr(), 64, None, gate.data_ptr(), None) == MQ_E_UNSUPPORTED
+    y = torch.empty((2, 64), device="cuda")
+    assert lib.mq_qmatmul(dev.handle, q4.handle, xq.data.data_ptr(), mold_amd._lib.MQ_X_Q8K, 2, 1024,
+                          y.data_ptr(), 0, 64, None, 0, None) == MQ_E_INVALID          # ldx != k
+    assert lib.mq_quantize_x_q8k(dev.handle, x.data_ptr(), 0, 2, 500, 512, xq.data.data_ptr(), None) == MQ_E_INVALID
+
+
 @pytest.mark.parametrize("m", [1, 3, 8])
 def test_gemv_q4k_exact_on_q8k_grid(dev, torch, m):
     """Activations already on a Q8_K grid: per super-block x = c * q with integer q in
