@@ -60,6 +60,8 @@ import math
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Optional, Tuple
 
+import numpy as np
+
 from .flux import apply_rope, attention_bf16, attention_bf16_batch, gelu_tanh, layer_norm, padded_len, run_guarded, silu, text_stream
 from .quantized import ACT_GELU_TANH, GgmlDType, Linear, QTensor
 
@@ -167,6 +169,62 @@ class QwenParams:
             elif name == "img_in.weight":
                 t = t.to(torch.bfloat16)
             dense[name] = t
+        return QwenParams(cfg, lin, dense)
+
+    @staticmethod
+    def from_gguf(cfg: QwenConfig, path: str, device) -> "QwenParams":
+        """The transformer's parameters from a GGUF file in mold's layout (the names
+        `qlinear` reads, qwen_image/quantized_transformer.rs:79-93, 584-611, 631-632,
+        679-687, 847-851, 972-973, 1011-1016: `<linear>.weight` / `.bias`, separate
+        `attn.to_q` / `to_k` / `to_v` and `add_q_proj` / `add_k_proj` / `add_v_proj`,
+        RmsNorm `.weight`s), read the way `VarBuilder::from_gguf` does
+        (qwen_image/pipeline.rs:936): every tensor to the device in one pipelined
+        call (mq_gguf_load_tensors).  The step's stacked q/k/v weights are the three
+        tensors concatenated by rows on the device (mq_qtensor_concat_rows; they must
+        share one type), biases dequantized to f32, img_in's weight (stored in any
+        type: its K = in_channels holds no 256-wide block) and the norm weights
+        dequantized to bf16.  No tensor byte passes through the host."""
+        import torch
+        from . import gguf
+        parts: Dict[str, Tuple[str, ...]] = {}
+        for name in linear_shapes(cfg):
+            if name.endswith("attn.to_qkv"):
+                p = name[:-len("to_qkv")]
+                parts[name] = (p + "to_q", p + "to_k", p + "to_v")
+            elif name.endswith("attn.add_qkv_proj"):
+                p = name[:-len("add_qkv_proj")]
+                parts[name] = (p + "add_q_proj", p + "add_k_proj", p + "add_v_proj")
+            else:
+                parts[name] = (name,)
+        need = [q + sfx for ps in parts.values() for q in ps for sfx in (".weight", ".bias")] + list(dense_shapes(cfg))
+        c = gguf.Content.read(path)
+        try:
+            missing = [nm for nm in need if nm not in c.tensor_infos]
+            if missing:
+                raise KeyError(f"{path}: tensors missing: {missing[:4]}")
+            qts = c.tensors(need, device)
+        finally:
+            c.close()
+        lin, dense = {}, {}
+        for name, (n, k, _) in linear_shapes(cfg).items():
+            ws = [qts[q + ".weight"] for q in parts[name]]
+            if any(w.shape[1] != k for w in ws) or sum(w.shape[0] for w in ws) != n:
+                raise ValueError(f"{name}: stored as {[w.shape for w in ws]}, the config needs ({n}, {k})")
+            if len({w.dtype() for w in ws}) != 1:
+                raise ValueError(f"{name}: {parts[name]} are stored as {[w.dtype().name for w in ws]}; "
+                                 "the stacked projection needs one type")
+            if not ws[0].dtype().is_quantized:
+                raise ValueError(f"{name} is dense {ws[0].dtype().name}; the step runs quantized linears")
+            w = ws[0] if len(ws) == 1 else QTensor.concat_rows(device, ws)
+            bias = torch.cat([qts[q + ".bias"].dequantize(torch.float32).reshape(-1) for q in parts[name]])
+            lin[name] = Linear(w, bias.contiguous())
+        for name, shape in dense_shapes(cfg).items():
+            t = qts[name]
+            want = (int(np.prod(shape[:-1])) if len(shape) > 1 else 1, shape[-1])
+            if t.shape != want:
+                raise ValueError(f"{name}: stored as {t.shape}, the config needs {tuple(shape)}")
+            dt = torch.float32 if name.endswith(".bias") else torch.bfloat16
+            dense[name] = t.dequantize(dt).reshape(shape)
         return QwenParams(cfg, lin, dense)
 
     def quantized_bytes(self) -> int:

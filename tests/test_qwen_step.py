@@ -219,6 +219,77 @@ def test_qwen_step_tiny_matches_dequantized_reference():
 
 
 @pytest.mark.gpu
+def test_qwen_step_from_mold_layout_gguf(tmp_path):
+    """A tiny-config Qwen-Image GGUF in mold's layout, written by an independent
+    restatement of the container (tests/gguf_ref.py): the config's quantized types per
+    role (Q3_K attention, Q2_K MLP, Q4_K elsewhere), separate to_q / to_k / to_v and
+    add_q_proj / add_k_proj / add_v_proj tensors, F32 biases and RmsNorm weights, a BF16
+    img_in weight, mold's tensor names, GGUF ne order.  QwenParams.from_gguf loads it
+    through the C ABI alone (one mq_gguf_load_tensors call, the q/k/v weights stacked on
+    the device by mq_qtensor_concat_rows), and the step matches the f64 restatement on
+    the file's own values within the 1e-2 bar."""
+    import mold_amd
+    from oracle import oracle as O
+    from . import gguf_ref as R
+    cfg = Q.QwenConfig.tiny()
+    print("[qwen] tiny step from a mold-layout GGUF", flush=True)
+    rng = np.random.default_rng(21)
+    tensors, W, D = [], {}, {}
+    for name, (n, k, role) in Q.linear_shapes(cfg).items():
+        t = int(cfg.qtype(role))
+        if name.endswith("attn.to_qkv") or name.endswith("attn.add_qkv_proj"):
+            p = name[: name.rindex(".") + 1]
+            subs = ["to_q", "to_k", "to_v"] if name.endswith("to_qkv") else ["add_q_proj", "add_k_proj", "add_v_proj"]
+            names, rows = [p + s_ for s_ in subs], [n // 3] * 3
+        else:
+            names, rows = [name], [n]
+        ws, bs = [], []
+        for nm, r in zip(names, rows):
+            w = (rng.standard_normal((r, k)) * 0.02).astype(np.float32)
+            blocks = O.quantize(t, w)
+            b = (rng.standard_normal(r) * 0.02).astype(np.float32)
+            tensors.append((nm + ".weight", t, (r, k), blocks))
+            tensors.append((nm + ".bias", O.F32, (r,), b.view(np.uint8)))
+            ws.append(torch.from_numpy(O.dequantize(t, blocks, r, k)))
+            bs.append(torch.from_numpy(b))
+        W[name] = (torch.cat(ws), torch.cat(bs))
+    for name, shape in Q.dense_shapes(cfg).items():
+        v = rng.standard_normal(shape).astype(np.float32) * 0.02
+        if name.endswith(".bias"):
+            tensors.append((name, O.F32, shape, v.view(np.uint8)))
+            D[name] = torch.from_numpy(v)
+            continue
+        if name != "img_in.weight":
+            v = v + 1.0
+        b16 = torch.from_numpy(v).to(torch.bfloat16)
+        tensors.append((name, O.BF16, shape, b16.view(torch.int16).numpy().view(np.uint8).reshape(-1)))
+        D[name] = b16.float()
+    path = str(tmp_path / "qwen-tiny-mixed.gguf")
+    R.write(path, [("general.architecture", 8, "qwen_image")], tensors)
+    dev = mold_amd.Device(0)
+    params = Q.QwenParams.from_gguf(cfg, path, dev)
+    for name, (n, k, role) in Q.linear_shapes(cfg).items():
+        qt = params.lin[name].matmul.w
+        assert qt.dtype() == cfg.qtype(role) and qt.shape == (n, k), name
+        assert torch.equal(params.lin[name].bias.cpu(), W[name][1]), name
+        if qt.shape[0] == n:   # the stacked weights are the parts' blocks in order
+            assert torch.equal(torch.from_numpy(O.dequantize(int(qt.dtype()), qt.data(), n, k)), W[name][0]), name
+    for name, t in D.items():
+        want = t if name.endswith(".bias") else t.to(torch.bfloat16)
+        assert torch.equal(params.dense[name].cpu().to(want.dtype), want), name
+    inp = Q.make_inputs(cfg, height=272, width=240, txt_len=40, device="cuda", seed=8)
+    out = Q.QwenImageStep(params).forward(**inp)
+    torch.cuda.synchronize()
+    ref = reference_forward(cfg, W, {k_: v.float() for k_, v in D.items()},
+                            {k_: (v.cpu() if hasattr(v, "cpu") else v) for k_, v in inp.items()})
+    o = out.cpu().numpy()
+    assert np.isfinite(o).all()
+    err = _rel(o, ref.numpy())
+    print(f"[qwen] GGUF-loaded step rel-L2 vs f64 reference: {err:.3e}", flush=True)
+    assert err <= STEP_TOL, err
+
+
+@pytest.mark.gpu
 def test_qwen_cfg_batch2_matches_two_single_forwards():
     """Batched CFG forward (cond + uncond along dim 0, the uncond prompt shorter
     and padded, its padding masked out of attention) against two batch-1 forwards
