@@ -408,9 +408,10 @@ int mq_gguf_kv_str(const mq_gguf *g, int64_t index, uint64_t elem, const char **
 }
 
 int mq_gguf_load_tensors(mq_ctx *ctx, const mq_gguf *g, const int64_t *indices, int64_t count, mq_qtensor **out) {
+  if (out)
+    for (int64_t i = 0; i < count; ++i) out[i] = nullptr;
   if (!g || !out || count < 0 || (count > 0 && !indices))
     return gfail(MQ_E_INVALID, "mq_gguf_load_tensors: bad argument");
-  for (int64_t i = 0; i < count; ++i) out[i] = nullptr;
   if (!ctx) return gfail(MQ_E_INVALID, "mq_gguf_load_tensors: NULL ctx");
   if (count == 0) return MQ_OK;
   std::vector<mq::UploadJob> jobs;

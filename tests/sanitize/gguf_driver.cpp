@@ -103,6 +103,9 @@ void walk(mq_gguf *g, bool strict) {
   CHECK(mq_gguf_load_tensors(ctx, g, bad, 2, outs.data()) == MQ_E_INVALID);
   CHECK(mq_gguf_load_tensors(ctx, g, nullptr, 1, outs.data()) == MQ_E_INVALID);
   CHECK(mq_gguf_load_tensors(nullptr, g, idx.data(), nt, outs.data()) == MQ_E_INVALID);
+  for (auto &o : outs) o = reinterpret_cast<mq_qtensor *>(&idx);
+  CHECK(mq_gguf_load_tensors(ctx, nullptr, idx.data(), nt, outs.data()) == MQ_E_INVALID);
+  for (int64_t i = 0; i < nt; ++i) CHECK(outs[(size_t)i] == nullptr);  // cleared on every failure
   CHECK(mq_gguf_tensor_info(g, nt, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr) == MQ_E_INVALID);
   CHECK(mq_gguf_kv_info(g, nkv, nullptr, nullptr, nullptr, nullptr) == MQ_E_INVALID);
 }
