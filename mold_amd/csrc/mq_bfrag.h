@@ -35,6 +35,12 @@ __device__ __forceinline__ float ub(uint32_t w) {
   return (float)((w >> (8 * E)) & 0xFFu);
 }
 
+// Signed byte e of w as f32.
+template <int E>
+__device__ __forceinline__ float sb(uint32_t w) {
+  return (float)(int8_t)(w >> (8 * E));
+}
+
 // The words reaching fma8 are already masked per byte; keeping them opaque
 // stops the compiler from folding that mask into each byte extraction, so
 // every byte converts with one v_cvt_f32_ubyte{0..3}.
@@ -45,13 +51,24 @@ __device__ __forceinline__ uint32_t opaque(uint32_t w) {
 
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
+// The eight weights of a fragment as u[i] * a + b before that fma is taken:
+// the f32 GEMV forms x . w as a * (x . u) + b * sum(x), which saves the
+// decode fma of every weight.
+struct Lin8 {
+  float u[8];
+  float a, b;
+};
+
 // Eight fma(byte_e(word), a, b) for the bytes of two words: the exact f32
-// weights (O = f32x8, the GEMV's), or those rounded to bf16 (O = bf16x8, the
-// MFMA B fragment).
+// weights (O = f32x8), those rounded to bf16 (O = bf16x8, the MFMA B
+// fragment), or the bytes and (a, b) unapplied (O = Lin8).
 template <typename O = bf16x8>
 __device__ __forceinline__ O fma8(uint32_t w0, uint32_t w1, float a, float b) {
   w0 = opaque(w0);
   w1 = opaque(w1);
+  if constexpr (__is_same(O, Lin8)) {
+    return Lin8{{ub<0>(w0), ub<1>(w0), ub<2>(w0), ub<3>(w0), ub<0>(w1), ub<1>(w1), ub<2>(w1), ub<3>(w1)}, a, b};
+  }
   float v[8];
   v[0] = __builtin_fmaf(ub<0>(w0), a, b);
   v[1] = __builtin_fmaf(ub<1>(w0), a, b);
@@ -426,7 +443,8 @@ template <>
 struct T<Q5_1> : T32<Q5_1> {};
 
 // ggml dequantize_row_q8_0: y[j] = qs[j] * d.  The signed byte is read as
-// u = q + 128 (xor 0x80) so that fma(u, d, -128 d) = q*d exactly.
+// u = q + 128 (xor 0x80) so that fma(u, d, -128 d) = q*d exactly; the Lin8
+// form takes q itself (a = d, b = 0).
 template <>
 struct T<Q8_0> {
   static constexpr int kUnitK = 128;
@@ -451,6 +469,11 @@ struct T<Q8_0> {
     const float d = h2f((uint16_t)r.d[G]);
     constexpr uint32_t X = 0x80808080u;
     const uint4 &q = r.q[G][S >> 1];
+    if constexpr (__is_same(O, Lin8)) {
+      // the signed bytes themselves (v_cvt_f32_i32 of a sign-extended byte), b = 0
+      const uint32_t w0 = opaque(w0of<S>(q)), w1 = opaque(w1of<S>(q));
+      return Lin8{{sb<0>(w0), sb<1>(w0), sb<2>(w0), sb<3>(w0), sb<0>(w1), sb<1>(w1), sb<2>(w1), sb<3>(w1)}, d, 0.f};
+    }
     return fma8<O>(w0of<S>(q) ^ X, w1of<S>(q) ^ X, d, -128.f * d);
   }
 };

@@ -532,13 +532,19 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
 // chunks and the next item's loads are issued before the current item is
 // computed.  x is staged to LDS by direct loads (in the shadow of the first
 // item's weight loads); the items' partials go to LDS and thread (row, m)
-// adds them in (unit, half) order (deterministic).
+// adds them in (unit, half) order (deterministic).  At m = 1 a fragment's
+// eight weights u[i] * a + b are not formed: its dot is a * (u . x) + b *
+// sum(x), with the sums of x over each aligned run of 8 staged in LDS beside
+// x (18 VALU operations per 8 weights instead of 24; at m = 2 that form
+// spills, and from m = 3 on its per-row terms outweigh the saved decode).
 constexpr int kFragThreads = 512;
-constexpr size_t kFragMaxLds = 96 * 1024;
+constexpr size_t kFragMaxLds = 160 * 1024;  // gfx950's LDS per workgroup
 constexpr int kFragMaxM = 4;  // larger m takes gemv_kernel
+constexpr int kFragLinMaxM = 1;
 
 __host__ __device__ inline size_t frag_lds_bytes(int64_t k, int m, int64_t rows, int64_t units) {
-  return (size_t)m * k * 4 + ((size_t)rows * units * 2 + 1) * m * 4;
+  const size_t sums = m <= kFragLinMaxM ? (size_t)m * (k / 8) * 4 : 0;
+  return (size_t)m * k * 4 + sums + ((size_t)rows * units * 2 + 1) * m * 4;
 }
 
 template <int TYPE, int M, typename OUT>
@@ -548,10 +554,13 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
                                                                  const float *__restrict__ bias, int act) {
   using TT = bfrag::T<TYPE>;
   constexpr int kU = TT::kUnitK, kP = kU / 64;
+  constexpr bool kLin = M <= kFragLinMaxM;
+  constexpr bool kLinAdd = TYPE != Q8_0;  // Q8_0's Lin8 form has b = 0
   extern __shared__ __align__(16) uint8_t smem[];
   const int64_t k = (int64_t)units * kU;
   float *xs = reinterpret_cast<float *>(smem);            // [M][k]
-  float *red = xs + (size_t)M * k;                        // [units * 2 * rows + 1][M]
+  float *sx = xs + (size_t)M * k;                         // [M][k / 8] (kLin)
+  float *red = sx + (kLin ? (size_t)M * (k >> 3) : 0);    // [units * 2 * rows + 1][M]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int64_t r0 = (int64_t)blockIdx.x * rows;
@@ -580,6 +589,16 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
     const int uh = p / rows, u = uh >> 1, h = uh & 1;
     typename TT::Sc sc;
     TT::prep(d, sc, h);
+    // chunk(S, h) = chunk(S, 0) + h * dh for every slice S of both chunk
+    // maps: the item's x (and run sums) start at one 32-bit LDS offset and
+    // each slice adds a constant
+    constexpr int dh = TT::chunk(0, 1) - TT::chunk(0, 0);
+    static_assert(TT::chunk(1, 1) - TT::chunk(1, 0) == dh && TT::chunk(2, 1) - TT::chunk(2, 0) == dh &&
+                  TT::chunk(3, 1) - TT::chunk(3, 0) == dh);
+    const int e0 = u * kU + 8 * dh * h;
+    const float *xi = xs + e0;
+    const float *si = sx + (e0 >> 3);
+    const int kk = units * kU;
     float acc[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.f;
@@ -587,22 +606,42 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
       // keeps the x reads of one step together with their use
       asm volatile("" ::: "memory");
       static_for<4>([&]<int S>() {
-        const bfrag::f32x8 v = TT::template frag<G, S, bfrag::f32x8>(d, sc);
-        const int64_t e = (int64_t)u * kU + 64 * G + 8 * (h ? TT::chunk(S, 1) : TT::chunk(S, 0));
+        constexpr int e = 64 * G + 8 * TT::chunk(S, 0);
+        if constexpr (kLin) {
+          const bfrag::Lin8 v = TT::template frag<G, S, bfrag::Lin8>(d, sc);
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          const float4 xa = *reinterpret_cast<const float4 *>(xs + m * k + e);
-          const float4 xb = *reinterpret_cast<const float4 *>(xs + m * k + e + 4);
-          float a = acc[m];
-          a = __builtin_fmaf(v[0], xa.x, a);
-          a = __builtin_fmaf(v[1], xa.y, a);
-          a = __builtin_fmaf(v[2], xa.z, a);
-          a = __builtin_fmaf(v[3], xa.w, a);
-          a = __builtin_fmaf(v[4], xb.x, a);
-          a = __builtin_fmaf(v[5], xb.y, a);
-          a = __builtin_fmaf(v[6], xb.z, a);
-          a = __builtin_fmaf(v[7], xb.w, a);
-          acc[m] = a;
+          for (int m = 0; m < M; ++m) {
+            const float4 xa = *reinterpret_cast<const float4 *>(xi + m * kk + e);
+            const float4 xb = *reinterpret_cast<const float4 *>(xi + m * kk + e + 4);
+            float t = v.u[0] * xa.x;
+            t = __builtin_fmaf(v.u[1], xa.y, t);
+            t = __builtin_fmaf(v.u[2], xa.z, t);
+            t = __builtin_fmaf(v.u[3], xa.w, t);
+            t = __builtin_fmaf(v.u[4], xb.x, t);
+            t = __builtin_fmaf(v.u[5], xb.y, t);
+            t = __builtin_fmaf(v.u[6], xb.z, t);
+            t = __builtin_fmaf(v.u[7], xb.w, t);
+            float a = __builtin_fmaf(v.a, t, acc[m]);
+            if constexpr (kLinAdd) a = __builtin_fmaf(v.b, si[m * (kk >> 3) + (e >> 3)], a);
+            acc[m] = a;
+          }
+        } else {
+          const bfrag::f32x8 v = TT::template frag<G, S, bfrag::f32x8>(d, sc);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            const float4 xa = *reinterpret_cast<const float4 *>(xi + m * kk + e);
+            const float4 xb = *reinterpret_cast<const float4 *>(xi + m * kk + e + 4);
+            float a = acc[m];
+            a = __builtin_fmaf(v[0], xa.x, a);
+            a = __builtin_fmaf(v[1], xa.y, a);
+            a = __builtin_fmaf(v[2], xa.z, a);
+            a = __builtin_fmaf(v[3], xa.w, a);
+            a = __builtin_fmaf(v[4], xb.x, a);
+            a = __builtin_fmaf(v[5], xb.y, a);
+            a = __builtin_fmaf(v[6], xb.z, a);
+            a = __builtin_fmaf(v[7], xb.w, a);
+            acc[m] = a;
+          }
         }
       });
     });
@@ -634,6 +673,16 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  if constexpr (kLin && kLinAdd) {
+    // sums of x over each aligned run of 8 (row m's run j at m * k / 8 + j)
+    const int nrun = (int)(M * (k >> 3));
+    for (int c = tid; c < nrun; c += kFragThreads) {
+      const float4 xa = *reinterpret_cast<const float4 *>(xs + 8 * (int64_t)c);
+      const float4 xb = *reinterpret_cast<const float4 *>(xs + 8 * (int64_t)c + 4);
+      sx[c] = ((xa.x + xa.y) + (xa.z + xa.w)) + ((xb.x + xb.y) + (xb.z + xb.w));
+    }
+    __syncthreads();
+  }
   if (kXFirst) load_item(tid, a);
 
   // 2. items, the next one's loads in flight while the current one computes
@@ -664,7 +713,6 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
 static int frag_rows(int type, int64_t n, int64_t k, int64_t m, int cus) {
   const int64_t unit = type == Q8_0 ? 128 : 256;
   if (type == Q4_K || k % 256 != 0 || m > kFragMaxM) return 0;
-  if ((type == Q5_K || type == Q6_K) && m > 3) return 0;  // their m = 4 instances spill
   int64_t rows = (n + cus - 1) / cus;
   if (rows < 1) rows = 1;
   while (rows > 8 && frag_lds_bytes(k, (int)m, rows, k / unit) > kFragMaxLds) rows = (rows + 1) / 2;

@@ -398,6 +398,27 @@ def test_gemv_q4k_odd_tile_counts_repeat_bit_identical(dev, torch, n, k, m):
     _gemv_check(t, x, y1.cpu().numpy(), blocks, n, k)
 
 
+FRAG_TYPES = [GgmlDType.Q8_0, GgmlDType.Q4_0, GgmlDType.Q4_1, GgmlDType.Q5_0, GgmlDType.Q5_K, GgmlDType.Q6_K,
+              GgmlDType.Q2_K, GgmlDType.Q3_K]
+
+
+@pytest.mark.parametrize("t", FRAG_TYPES, ids=lambda t: t.name)
+@pytest.mark.parametrize("m", [1, 2, 3])
+def test_gemv_long_k_offset_x(dev, torch, t, m):
+    """The f32 GEMV at K = 10240 (x, and at m = 1 its sums over runs of 8, fill
+    most of the workgroup's LDS) on x with a common offset, x = 4 + N(0, 1): at
+    m = 1 each fragment's dot is a * (u . x) + b * sum(x), and the offset makes
+    the b * sum(x) term the large part of every partial.  Held to f64 like every
+    other GEMV (1e-5 for these types)."""
+    n, k = 96, 10240
+    _say(f"gemv long K offset x {t.name} m={m}")
+    blocks = _weights(int(t), n, k, seed=17 + m)
+    qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+    x = (4.0 + np.random.default_rng(300 + m).standard_normal((m, k))).astype(np.float32)
+    y = QMatMul(qt).forward(torch.from_numpy(x).cuda()).cpu().numpy()
+    _gemv_check(t, x, y, blocks, n, k)
+
+
 def test_gemv_ksplit_large_k(dev, torch):
     # few row tiles, long K: the launcher splits K across workgroups
     t, n, k, m = GgmlDType.Q4_K, 64, 256 * 48, 4
