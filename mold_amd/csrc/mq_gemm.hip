@@ -632,10 +632,20 @@ template hipError_t launch_gemm_type<MQ_GEMM_TYPE>(const WView &, int64_t, int64
 #else  // the type dispatcher
 
 // Tail plan of the fast kernel: when the last round of tiles over the CUs'
-// workgroup slots is partial, split each of those tail tiles into kp K parts
-// so that they fill one round.
-// K parts of each tail tile for row tiles of fm (1: no split).
-static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, int fm, int64_t *rem_out) {
+// workgroup slots is partial, split each of those tail tiles into kp K parts.
+// K parts of each tail tile for row tiles of fm (1: no split).  fill: the
+// tail fills one round of the slots (the measure gemm_tile_m compares row
+// tiles by).  The split a launch runs (!fill) is the same for 256-row tiles
+// (one workgroup per CU); the 64- and 128-row tiles (four / three slots per
+// CU) split to about two workgroups per CU instead, and 128-row parts walk at
+// least three K units: each part walks more of K and the tail writes fewer
+// partial sums (same-box sweeps at m = 77 .. 1024: T5 q / up at m = 512 / 77
+// -8 / -13 %, FLUX text proj at m = 512 -10 %, Qwen text Q3_K / Q4_K at
+// m = 256 / 77 -12 / -14 / -11 %, 768 x 3072 -> 3072 Q4_K -17 %; a Q5_K
+// m = 77 with 64-row parts of three units, and 256-row tiles kept to three
+// units, measured slower).
+static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, int fm, int64_t *rem_out,
+                           bool fill) {
   const int fn = gemm_tile_n(fm);
   const int64_t tiles = ((m + fm - 1) / fm) * ((n + fn - 1) / fn);
   const int64_t slots = (int64_t)cus * gemm_wgs_per_cu(fm);
@@ -643,8 +653,10 @@ static int64_t tail_kparts(int type, int64_t m, int64_t n, int64_t k, int cus, i
   const int64_t units = k / gemm_unit_k(type);
   if (rem_out) *rem_out = rem;
   if (rem == 0 || units < 2) return 1;
-  int64_t kp = slots / rem;  // K parts per tail tile: they fill one round
-  kp = kp < units ? kp : units;
+  const bool two = !fill && fm != 256;
+  int64_t kp = (two ? 2 * (int64_t)cus : slots) / rem;  // workgroups the tail aims at, per tail tile
+  const int64_t max_parts = !fill && fm == 128 ? units / 3 : units;
+  kp = kp < max_parts ? kp : max_parts;
   kp = kp < kGemmMaxKParts ? kp : kGemmMaxKParts;
   return kp < 2 ? 1 : kp;
 }
@@ -671,8 +683,8 @@ int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus) {
     // 2-7 % slower with 128 rows, every large shape 3-18 % slower).
     const int64_t t256 = ((m + 255) / 256) * ((n + gemm_tile_n(256) - 1) / gemm_tile_n(256));
     if (t256 >= (int64_t)cus * gemm_wgs_per_cu(256)) return 256;
-    const int64_t kp256 = tail_kparts(type, m, n, k, cus, 256, nullptr);
-    const int64_t kp128 = tail_kparts(type, m, n, k, cus, 128, nullptr);
+    const int64_t kp256 = tail_kparts(type, m, n, k, cus, 256, nullptr, true);
+    const int64_t kp128 = tail_kparts(type, m, n, k, cus, 128, nullptr, true);
     if ((t256 <= cus / 4 && k <= 4096) || (kp256 >= 2 && kp128 == 1)) return 128;
     return 256;
   }
@@ -681,7 +693,7 @@ int gemm_tile_m(int type, int64_t m, int64_t n, int64_t k, int cus) {
   int best = 64;
   int64_t best_depth = -1;
   for (int fm : {64, 128}) {
-    const int64_t kp = tail_kparts(type, m, n, k, cus, fm, nullptr);
+    const int64_t kp = tail_kparts(type, m, n, k, cus, fm, nullptr, true);
     const int64_t depth = (units + kp - 1) / kp;
     if (best_depth < 0 || depth < best_depth) {
       best = fm;
@@ -698,7 +710,7 @@ GemmTail gemm_tail_plan(int type, int64_t m, int64_t n, int64_t k, int cus, bool
   GemmTail t{(int)tiles, 1, fm};
   if (!split) return t;
   int64_t rem = 0;
-  const int64_t kp = tail_kparts(type, m, n, k, cus, fm, &rem);
+  const int64_t kp = tail_kparts(type, m, n, k, cus, fm, &rem, false);
   if (kp < 2) return t;
   t.full_tiles = (int)(tiles - rem);
   t.kparts = (int)kp;
