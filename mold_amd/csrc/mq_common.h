@@ -128,21 +128,28 @@ __device__ __forceinline__ const uint8_t *fptr(const WView &w, int64_t t, int64_
   return w.base + field_offset(w.plane[F], SIZE, w.nb, t, b, r, j);
 }
 
-// 6-bit scale and min j of a Q4_K / Q5_K super-block (ggml get_scale_min_k4).
-__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, int &sc, int &mn) {
-  if (j < 4) {
-    sc = q[j] & 63;
-    mn = q[j + 4] & 63;
-  } else {
-    sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
-    mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
-  }
+// 6-bit scale and min j of a Q4_K / Q5_K super-block (ggml get_scale_min_k4)
+// from its 12 scale bytes as little-endian words s0, s1, s2.  For j < 4 they
+// are the low 6 bits of bytes j and j + 4; for j >= 4 the nibbles of byte j + 4
+// with the top 2 bits of bytes j - 4 and j: all eight at once as the bytes of
+// four words, then byte j & 3 of the pair for j (word operations throughout:
+// indexing the 12 bytes by a run-time j cost the dequantizer most of its time).
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, int &sc, int &mn) {
+  const uint32_t scw = j < 4 ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+  const uint32_t mw = j < 4 ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+  const int sh = 8 * (j & 3);
+  sc = (int)((scw >> sh) & 0xFFu);
+  mn = (int)((mw >> sh) & 0xFFu);
 }
 
-// Six-bit Q3_K scale j (0..15), still offset by 32 (ggml dequantize_row_q3_K).
-__device__ __forceinline__ int q3k_scale(int j, const uint8_t *s) {
-  const int low = j < 8 ? (s[j] & 0xF) : (s[j - 8] >> 4);
-  const int high = (s[8 + (j & 3)] >> (2 * (j >> 2))) & 3;
+// Six-bit Q3_K scale j (0..15), still offset by 32 (ggml dequantize_row_q3_K),
+// from the 12 scale bytes as words s0, s1, s2: the low 4 bits are the low
+// (j < 8) or high nibble of byte j & 7, the high 2 bits are bits 2 (j >> 2)
+// and up of byte 8 + (j & 3).
+__device__ __forceinline__ int q3k_scale(int j, uint32_t s0, uint32_t s1, uint32_t s2) {
+  const uint32_t lw = ((j & 4) ? s1 : s0) >> (4 * (j >> 3));
+  const int low = (int)((lw >> (8 * (j & 3))) & 0xFu);
+  const int high = (int)((s2 >> (8 * (j & 3) + 2 * (j >> 2))) & 3u);
   return low | (high << 4);
 }
 
@@ -242,14 +249,7 @@ template <>
 __device__ __forceinline__ void decode8<Q3_K>(const WView &w, int64_t t, int r, int64_t b, int e0, float out[8]) {
   const float d = h2f(ld<uint16_t>(fptr<3, 2>(w, t, b, r, 0)));
   const uint8_t *sp = fptr<2, 12>(w, t, b, r, 0);
-  uint8_t s[12];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const uint32_t v = ld<uint32_t>(sp + 4 * i);
-    s[4 * i + 0] = v & 0xFF; s[4 * i + 1] = (v >> 8) & 0xFF;
-    s[4 * i + 2] = (v >> 16) & 0xFF; s[4 * i + 3] = v >> 24;
-  }
-  const float dl = d * (float)(q3k_scale(e0 >> 4, s) - 32);
+  const float dl = d * (float)(q3k_scale(e0 >> 4, ld<uint32_t>(sp), ld<uint32_t>(sp + 4), ld<uint32_t>(sp + 8)) - 32);
   const int byte0 = 32 * (e0 >> 7) + (e0 & 31);
   const int sh = 2 * ((e0 & 127) >> 5);
   const uint2 q = ld<uint2>(fptr<1, 64>(w, t, b, r, byte0));
@@ -270,15 +270,8 @@ __device__ __forceinline__ void decode8_k45(const WView &w, int64_t t, int r, in
   const uint32_t dm = ld<uint32_t>(fptr<0, 4>(w, t, b, r, 0));
   const float d = h2f((uint16_t)(dm & 0xFFFF)), dmin = h2f((uint16_t)(dm >> 16));
   const uint8_t *sp = fptr<1, 12>(w, t, b, r, 0);
-  uint8_t s[12];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const uint32_t v = ld<uint32_t>(sp + 4 * i);
-    s[4 * i + 0] = v & 0xFF; s[4 * i + 1] = (v >> 8) & 0xFF;
-    s[4 * i + 2] = (v >> 16) & 0xFF; s[4 * i + 3] = v >> 24;
-  }
   int sc, mn;
-  scale_min_k4(e0 >> 5, s, sc, mn);
+  scale_min_k4(e0 >> 5, ld<uint32_t>(sp), ld<uint32_t>(sp + 4), ld<uint32_t>(sp + 8), sc, mn);
   const float d1 = d * (float)sc, m1 = dmin * (float)mn;
   const int g = e0 >> 6, hi = (e0 >> 5) & 1, l0 = e0 & 31;
   const uint2 q = ld<uint2>(fptr<FIVE ? 3 : 2, 128>(w, t, b, r, 32 * g + l0));
