@@ -642,7 +642,8 @@ int mq_qtensor_upload(mq_ctx *ctx, int dtype, int64_t n, int64_t k, const void *
 }
 
 // Shared by mq_quantize and mq_quantize_fp8: quantize src (f32 or FP8 E4M3
-// bytes) on `stream` into the upload staging buffer, then repack.
+// bytes) on `stream`, the 32-element block types straight into the tensor's
+// device layout, the k-quants into the upload staging buffer, then repack.
 static int quantize_common(mq_ctx *ctx, const char *fn, int dtype, int64_t n, int64_t k, const void *src, bool fp8,
                            int64_t ld, float scale, void *stream, mq_qtensor **out) {
   if (!ctx || !out || !src) return fail(MQ_E_INVALID, "%s: NULL argument", fn);
@@ -672,8 +673,22 @@ static int quantize_common(mq_ctx *ctx, const char *fn, int dtype, int64_t n, in
   const TypeInfo ti = type_info(dtype);
   if (k % ti.bs != 0) return fail(MQ_E_INVALID, "%s needs k %% %d == 0, got k=%lld", ti.name, ti.bs, (long long)k);
   DeviceGuard g(ctx->device);
-  const size_t nbytes = gguf_row_bytes(dtype, k) * (size_t)n;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (quantize_tiled_ok(dtype)) {
+    // 32-element block types: quantized straight into the device layout
+    mq_qtensor *t = nullptr;
+    int rc = make_tensor(ctx, dtype, n, k, &t);
+    if (rc) return rc;
+    hipError_t e = launch_quantize_tiled(dtype, src, fp8, ld, scale, t->data, t->geo, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      mq_qtensor_free(t);
+      return hip_fail(e, "quantize");
+    }
+    *out = t;
+    return MQ_OK;
+  }
+  const size_t nbytes = gguf_row_bytes(dtype, k) * (size_t)n;
   uint8_t *st = nullptr;
   int rc = device_stage(ctx, nbytes, &st);
   if (rc) return rc;

@@ -19,6 +19,11 @@ hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, in
 // Same from FP8 E4M3 bytes src[n, ld] (decoded exactly, times scale).
 hipError_t launch_quantize_fp8(int type, const uint8_t *src, int64_t ld, int64_t n, int64_t k, float scale,
                                void *dst_raw, hipStream_t stream);
+// The 32-element block types (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0) quantized straight
+// into a tensor's device layout (geometry g), f32 or FP8 E4M3 source.
+bool quantize_tiled_ok(int type);
+hipError_t launch_quantize_tiled(int type, const void *src, bool fp8, int64_t ld, float scale, void *tiled,
+                                 const Geo &g, hipStream_t stream);
 hipError_t launch_dequant(int type, const WView &w, int64_t n, int64_t k, void *dst, int dst_type,
                           hipStream_t stream);
 // Dense GGUF tensors (F32 / F16 / BF16): src[n, lds] of src_type -> dst[n,

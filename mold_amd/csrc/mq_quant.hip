@@ -16,6 +16,8 @@
 // make_qkx2_quants.  Q4_0/Q4_1/Q5_0/Q5_1/Q8_0 have a single formula.
 // One thread quantizes one block; raw blocks go to a staging buffer that the
 // upload path then permutes into the tiled device layout.
+#include <utility>
+
 #include "mq_kernels.h"
 
 #pragma clang fp contract(off)
@@ -541,6 +543,15 @@ __device__ __forceinline__ void quant_block(const float *x, uint8_t *o) {
   else q_q6_K(x, o);
 }
 
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_q_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f.template operator()<I>(), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for_q(F &&f) {
+  static_for_q_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // FP8 E4M3 ("fn": bias 7, no infinities, S.1111.111 is NaN) to f32, exact.
 __device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
   const uint32_t sign = (uint32_t)(b & 0x80) << 24;
@@ -554,27 +565,186 @@ __device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
 }
 
 // One thread per block: copy the block's inputs to private memory (f32 as
-// given, or FP8 E4M3 decoded exactly and multiplied by `scale`), quantize into
-// a private block image, store it to the raw staging buffer.
-template <int TYPE, bool FP8>
+// given, or FP8 E4M3 decoded exactly and multiplied by `scale`; with VEC the
+// rows are 16-byte aligned and the inputs come as 16-byte loads), quantize
+// into a private block image and put it in LDS; the workgroup's 64 blocks,
+// contiguous in the raw staging buffer, then leave as 16-byte stores (one
+// byte store per output byte had left the FP8 -> Q8_0 pass at ~7 % of HBM).
+template <int TYPE, bool FP8, bool VEC>
 __global__ __launch_bounds__(64) void quantize_kernel(const void *__restrict__ src, int64_t ld, int64_t n,
                                                       int64_t nb, float scale, uint8_t *__restrict__ dst) {
   constexpr TypeInfo ti = type_info(TYPE);
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n * nb) return;
-  const int64_t row = i / nb, b = i - row * nb;
-  float x[ti.bs];
-  if constexpr (FP8) {
-    const uint8_t *p = static_cast<const uint8_t *>(src) + row * ld + b * ti.bs;
-    for (int j = 0; j < ti.bs; ++j) x[j] = e4m3_to_f32(p[j]) * scale;
-  } else {
-    const float *p = static_cast<const float *>(src) + row * ld + b * ti.bs;
-    for (int j = 0; j < ti.bs; ++j) x[j] = p[j];
+  __shared__ __align__(16) uint8_t stage[64 * ti.ts];
+  const int64_t total = n * nb;
+  const int64_t i0 = (int64_t)blockIdx.x * 64;
+  const int64_t i = i0 + threadIdx.x;
+  if (i < total) {
+    const int64_t row = i / nb, b = i - row * nb;
+    float x[ti.bs];
+    if constexpr (FP8) {
+      const uint8_t *p = static_cast<const uint8_t *>(src) + row * ld + b * ti.bs;
+      if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < ti.bs / 16; ++c) {
+          const uint4 v = reinterpret_cast<const uint4 *>(p)[c];
+          const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int j = 0; j < 16; ++j) x[16 * c + j] = e4m3_to_f32((uint8_t)(wd[j >> 2] >> (8 * (j & 3)))) * scale;
+        }
+      } else {
+        for (int j = 0; j < ti.bs; ++j) x[j] = e4m3_to_f32(p[j]) * scale;
+      }
+    } else {
+      const float *p = static_cast<const float *>(src) + row * ld + b * ti.bs;
+      if constexpr (VEC) {
+#pragma unroll
+        for (int c = 0; c < ti.bs / 4; ++c) {
+          const float4 v = reinterpret_cast<const float4 *>(p)[c];
+          x[4 * c] = v.x;
+          x[4 * c + 1] = v.y;
+          x[4 * c + 2] = v.z;
+          x[4 * c + 3] = v.w;
+        }
+      } else {
+        for (int j = 0; j < ti.bs; ++j) x[j] = p[j];
+      }
+    }
+    uint8_t o[ti.ts];
+    quant_block<TYPE>(x, o);
+    for (int j = 0; j < ti.ts; ++j) stage[threadIdx.x * ti.ts + j] = o[j];
   }
-  uint8_t o[ti.ts];
-  quant_block<TYPE>(x, o);
-  uint8_t *q = dst + i * ti.ts;
-  for (int j = 0; j < ti.ts; ++j) q[j] = o[j];
+  __syncthreads();
+  // blocks i0 .. i0 + nblk - 1 are bytes i0 * ts .. of dst (i0 * ts is a
+  // multiple of 64 * ts, so 16-byte aligned in the 256-byte aligned buffer)
+  const int64_t nblk = total - i0 < 64 ? total - i0 : 64;
+  const int bytes = (int)nblk * ti.ts;
+  uint8_t *q = dst + i0 * ti.ts;
+  const int whole = bytes & ~15;
+  for (int o = 16 * (int)threadIdx.x; o < whole; o += 16 * 64)
+    *reinterpret_cast<uint4 *>(q + o) = *reinterpret_cast<const uint4 *>(stage + o);
+  for (int o = whole + (int)threadIdx.x; o < bytes; o += 64) q[o] = stage[o];
+}
+
+// A block image's bytes [OFF, OFF + 4) as a little-endian word (constant
+// offsets, so the image stays in registers).
+template <int OFF>
+__device__ __forceinline__ uint32_t image_word(const uint8_t *o) {
+  return (uint32_t)o[OFF] | ((uint32_t)o[OFF + 1] << 8) | ((uint32_t)o[OFF + 2] << 16) | ((uint32_t)o[OFF + 3] << 24);
+}
+
+// Field F of a block image into the tiled planes at (tile-block tb, row r):
+// a 16-byte column per chunk of a chunked field, one run for a record (the
+// same places the repack writes).
+template <int TYPE, int F>
+__device__ __forceinline__ void store_field(uint8_t *tiled, const Geo &g, int64_t tb, int r, const uint8_t *o) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  constexpr int size = ti.f[F].size, off = ti.f[F].off;
+  if constexpr (size % 16 == 0) {
+    static_for_q<size / 16>([&]<int C>() {
+      const uint4 v = make_uint4(image_word<off + 16 * C>(o), image_word<off + 16 * C + 4>(o),
+                                 image_word<off + 16 * C + 8>(o), image_word<off + 16 * C + 12>(o));
+      *reinterpret_cast<uint4 *>(tiled + g.plane[F] + ((tb * (size / 16) + C) * kRowTile + r) * 16) = v;
+    });
+  } else if constexpr (size == 4) {
+    *reinterpret_cast<uint32_t *>(tiled + g.plane[F] + (tb * kRowTile + r) * 4) = image_word<off>(o);
+  } else {
+    static_assert(size == 2, "record fields of the 32-element types are 2 or 4 bytes");
+    *reinterpret_cast<uint16_t *>(tiled + g.plane[F] + (tb * kRowTile + r) * 2) =
+        (uint16_t)((uint32_t)o[off] | ((uint32_t)o[off + 1] << 8));
+  }
+}
+
+// The 32-element types straight into the device layout: one 64-thread
+// workgroup per (4 consecutive blocks, 64-row tile t); thread r quantizes row
+// t * 64 + r's blocks (a 128-byte run of FP8 or 512 bytes of f32: whole cache
+// lines; rows past n: zeros, as the repack writes them) and stores each
+// block's fields where the repack would put them, so there is no raw staging
+// and no repack pass (the repack reads these 18-34-byte blocks 2 bytes at a
+// time).
+constexpr int kQtBlocks = 4;
+
+template <int TYPE, bool FP8, bool VEC>
+__global__ __launch_bounds__(64) void quantize_tiled_kernel(const void *__restrict__ src, int64_t ld, Geo g,
+                                                            float scale, uint8_t *__restrict__ tiled) {
+  constexpr TypeInfo ti = type_info(TYPE);
+  static_assert(ti.bs == 32, "32-element block types only");
+  const int64_t t = blockIdx.y;
+  const int r = threadIdx.x;
+  const int64_t row = t * kRowTile + r;
+#pragma unroll
+  for (int j = 0; j < kQtBlocks; ++j) {
+    const int64_t b = (int64_t)blockIdx.x * kQtBlocks + j;
+    if (b >= g.nb) break;  // uniform across the workgroup
+    uint8_t o[ti.ts];
+    if (row < g.n) {
+      float x[32];
+      if constexpr (FP8) {
+        const uint8_t *p = static_cast<const uint8_t *>(src) + row * ld + b * 32;
+        if constexpr (VEC) {
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[c];
+            const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[16 * c + i] = e4m3_to_f32((uint8_t)(wd[i >> 2] >> (8 * (i & 3)))) * scale;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) x[i] = e4m3_to_f32(p[i]) * scale;
+        }
+      } else {
+        const float *p = static_cast<const float *>(src) + row * ld + b * 32;
+        if constexpr (VEC) {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const float4 v = reinterpret_cast<const float4 *>(p)[c];
+            x[4 * c] = v.x;
+            x[4 * c + 1] = v.y;
+            x[4 * c + 2] = v.z;
+            x[4 * c + 3] = v.w;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) x[i] = p[i];
+        }
+      }
+      quant_block<TYPE>(x, o);
+    } else {
+#pragma unroll
+      for (int i = 0; i < ti.ts; ++i) o[i] = 0;
+    }
+    const int64_t tb = t * g.nb + b;
+    static_for_q<ti.nf>([&]<int F>() { store_field<TYPE, F>(tiled, g, tb, r, o); });
+  }
+}
+
+template <bool FP8>
+hipError_t launch_quantize_tiled_src(int type, const void *src, int64_t ld, float scale, void *tiled, const Geo &g,
+                                     hipStream_t stream) {
+  if (g.n == 0 || g.nb == 0) return hipSuccess;
+  const int64_t es = FP8 ? 1 : 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (ld * es) % 16 == 0;
+  const dim3 grid((unsigned)((g.nb + kQtBlocks - 1) / kQtBlocks), (unsigned)g.ntiles);
+  bool ok = false;
+  auto go = [&]<int T>() {
+    if (vec)
+      hipLaunchKernelGGL((quantize_tiled_kernel<T, FP8, true>), grid, dim3(64), 0, stream, src, ld, g, scale,
+                         static_cast<uint8_t *>(tiled));
+    else
+      hipLaunchKernelGGL((quantize_tiled_kernel<T, FP8, false>), grid, dim3(64), 0, stream, src, ld, g, scale,
+                         static_cast<uint8_t *>(tiled));
+    ok = true;
+  };
+  switch (type) {
+    case Q4_0: go.template operator()<Q4_0>(); break;
+    case Q4_1: go.template operator()<Q4_1>(); break;
+    case Q5_0: go.template operator()<Q5_0>(); break;
+    case Q5_1: go.template operator()<Q5_1>(); break;
+    case Q8_0: go.template operator()<Q8_0>(); break;
+    default: break;
+  }
+  if (!ok) return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 template <bool FP8>
@@ -584,10 +754,18 @@ hipError_t launch_quantize_src(int type, const void *src, int64_t ld, int64_t n,
   const int64_t nb = k / ti.bs;
   const int64_t total = n * nb;
   if (total == 0) return hipSuccess;
+  if ((reinterpret_cast<uintptr_t>(dst_raw) & 15) != 0) return hipErrorInvalidValue;
+  // 16-byte source loads need every block's first element 16-byte aligned
+  const int64_t es = FP8 ? 1 : 4;
+  const bool vec = (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (ld * es) % 16 == 0 && (ti.bs * es) % 16 == 0;
   const unsigned grid = (unsigned)((total + 63) / 64);
   bool ok = dispatch_type(type, [&]<int T>() {
-    hipLaunchKernelGGL((quantize_kernel<T, FP8>), dim3(grid), dim3(64), 0, stream, src, ld, n, nb, scale,
-                       static_cast<uint8_t *>(dst_raw));
+    if (vec)
+      hipLaunchKernelGGL((quantize_kernel<T, FP8, true>), dim3(grid), dim3(64), 0, stream, src, ld, n, nb, scale,
+                         static_cast<uint8_t *>(dst_raw));
+    else
+      hipLaunchKernelGGL((quantize_kernel<T, FP8, false>), dim3(grid), dim3(64), 0, stream, src, ld, n, nb, scale,
+                         static_cast<uint8_t *>(dst_raw));
   });
   if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
@@ -603,6 +781,14 @@ hipError_t launch_quantize(int type, const float *src, int64_t ld, int64_t n, in
 hipError_t launch_quantize_fp8(int type, const uint8_t *src, int64_t ld, int64_t n, int64_t k, float scale,
                                void *dst_raw, hipStream_t stream) {
   return launch_quantize_src<true>(type, src, ld, n, k, scale, dst_raw, stream);
+}
+
+bool quantize_tiled_ok(int type) { return type == Q4_0 || type == Q4_1 || type == Q5_0 || type == Q5_1 || type == Q8_0; }
+
+hipError_t launch_quantize_tiled(int type, const void *src, bool fp8, int64_t ld, float scale, void *tiled,
+                                 const Geo &g, hipStream_t stream) {
+  return fp8 ? launch_quantize_tiled_src<true>(type, src, ld, scale, tiled, g, stream)
+             : launch_quantize_tiled_src<false>(type, src, ld, 1.0f, tiled, g, stream);
 }
 
 }  // namespace mq
