@@ -430,6 +430,51 @@ def test_gemv_ksplit_large_k(dev, torch):
     _gemv_check(t, x, y, blocks, n, k)
 
 
+@pytest.mark.parametrize("t", TYPES, ids=IDS)
+def test_tiny_shapes_brute_force(dev, torch, t):
+    """Every combination of small shapes: m in {1, 3, 9, 33} (both sides of the
+    GEMV / GEMM switch at m = 8), n in {1, 33, 65} (a single row in a padded
+    64-row tile, and one row past a tile), and k of one and three blocks plus,
+    for the 32-element types, one 256-element unit and a block (K below or off
+    the fast kernels' unit: the generic kernels).  Every output finite and
+    bit-identical on a repeat.  A single output's relative error says little
+    (one dot can be near zero), so for each k the outputs of all (m, n) pairs of
+    a path are pooled and held to that path's rel-L2 bar against the f64
+    dequantize-then-matmul (GEMV 1e-5 on exact weights, the Q4_K Q8_K GEMV and
+    the GEMM 1e-2), and every Q4_K GEMV output also to its Q8_K error bound."""
+    bs = O.block_size(int(t))
+    ks = [bs, 3 * bs] + ([256 + bs] if bs == 32 else [])
+    for k in ks:
+        pooled = {"gemv": ([], []), "gemm": ([], [])}
+        for n in (1, 33, 65):
+            blocks = _weights(int(t), n, k, seed=7 * n + k)
+            qt = QTensor.from_blocks(dev, t, (n, k), blocks)
+            mm = QMatMul(qt)
+            for m in (1, 3, 9, 33):
+                _say(f"tiny {t.name} m={m} n={n} k={k}")
+                x = np.random.default_rng(m + n + k).standard_normal((m, k)).astype(np.float32)
+                xt = torch.from_numpy(x).cuda()
+                y = mm.forward(xt)
+                y2 = mm.forward(xt)
+                torch.cuda.synchronize()
+                assert torch.equal(y.view(torch.int32), y2.view(torch.int32)), (m, n, k)
+                yn = y.cpu().numpy()
+                assert np.isfinite(yn).all(), (m, n, k)
+                ref = O.matmul_f64(int(t), x, blocks, n, k)
+                path = "gemv" if m <= 8 else "gemm"
+                pooled[path][0].append(yn.ravel())
+                pooled[path][1].append(ref.ravel())
+                if path == "gemv" and int(t) == O.Q4_K:
+                    err = np.abs(yn.astype(np.float64) - ref)
+                    bound = _q8k_row_bound(x, blocks, int(t), n, k)
+                    assert (err <= bound).all(), (m, n, k, float((err / bound).max()))
+        for path, (ys, refs) in pooled.items():
+            err = O.rel_l2(np.concatenate(ys), np.concatenate(refs))
+            tol = GEMV_TOL if path == "gemv" and int(t) != O.Q4_K else GEMM_TOL
+            print(f"[case] {t.name} k={k} {path} pooled rel-L2 {err:.2e}", flush=True)
+            assert err <= tol, (path, k, err)
+
+
 # --------------------------------------------------------------------- GEMM
 
 @pytest.mark.parametrize("t", TYPES, ids=IDS)
