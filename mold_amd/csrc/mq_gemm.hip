@@ -440,7 +440,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
-        if (colok && row0 + ro < m) yc[ro * ldy] = __builtin_fmaf(g, apply_act(acc[mb][e] + bv, act), r[mb & 1][e]);
+        if (colok && row0 + ro < m) yc[ro * ldy] = __builtin_fmaf(g, act_out<float>(acc[mb][e] + bv, act), r[mb & 1][e]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -544,7 +544,7 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (col0 + j < n)
-          yr[j] = __builtin_fmaf(gate[col0 + j], apply_act(sv[j] + (bias ? bias[col0 + j] : 0.f), act), rv[j]);
+          yr[j] = __builtin_fmaf(gate[col0 + j], act_out<float>(sv[j] + (bias ? bias[col0 + j] : 0.f), act), rv[j]);
       return;
     }
   }

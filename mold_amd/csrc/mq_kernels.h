@@ -120,13 +120,15 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
-// The same GELU-tanh for bf16 outputs: 0.5 v (1 + tanh u) = v / (1 + e^(-2u)),
-// u = sqrt(2/pi) (v + 0.044715 v^3), written as v / (1 + 2^(v (K0 + K1 v^2)))
-// with K0 = -2 sqrt(2/pi) / ln 2 and K1 = 0.044715 K0 folded, and evaluated
-// with the hardware base-2 exponential and reciprocal: five ALU operations
-// and two transcendentals, relative error about 1e-6, far below bf16's 2^-8
-// rounding step.  Large |v| saturate correctly (2^z -> 0 gives v, -> inf gives
-// 0).  f32 outputs keep apply_act.
+// The same GELU-tanh for the GEMM's epilogues: 0.5 v (1 + tanh u) =
+// v / (1 + e^(-2u)), u = sqrt(2/pi) (v + 0.044715 v^3), written as
+// v / (1 + 2^(v (K0 + K1 v^2))) with K0 = -2 sqrt(2/pi) / ln 2 and K1 = 0.044715
+// K0 folded, and evaluated with the hardware base-2 exponential and
+// reciprocal: five ALU operations and two transcendentals, relative error
+// about 1e-6, far below bf16's 2^-8 rounding step and below the bf16-input
+// GEMM's own error for f32 outputs (apply_act's tanhf made the f32 GELU
+// epilogue 12-19 % of the launch).  Large |v| saturate correctly (2^z -> 0
+// gives v, -> inf gives 0).  The GEMVs, exact to 1e-5, keep apply_act.
 __device__ __forceinline__ float gelu_fast(float v) {
   constexpr float K0 = -2.302208198144325f, K1 = -0.1029432395800235f;
   const float z = v * __builtin_fmaf(v * v, K1, K0);
@@ -134,11 +136,7 @@ __device__ __forceinline__ float gelu_fast(float v) {
 }
 template <typename OUT>
 __device__ __forceinline__ float act_out(float v, int act) {
-  if constexpr (std::is_same_v<OUT, __bf16>) {
-    return act == 1 ? gelu_fast(v) : v;
-  } else {
-    return apply_act(v, act);
-  }
+  return act == 1 ? gelu_fast(v) : v;
 }
 
 }  // namespace mq
