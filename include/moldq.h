@@ -241,6 +241,26 @@ int mq_qk_norm_rope(const void *qkv, int qkv_dtype, int64_t ld, int64_t rows, in
                     const float *sin_table, void *q_out, void *k_out, void *v_out, int64_t row_off, int64_t l_total,
                     void *stream);
 
+/* Correction of an attention computed over zero-padded keys.  o is the bf16
+ * attention output [batch, heads, >= rows, 128] (element strides
+ * o_batch_stride / o_head_stride / o_row_stride, unit stride along the head
+ * dim), lse its f32 log-sum-exp [batch, heads, >= rows] (unit stride along
+ * rows), npad f32 [batch] the zero keys (padding plus masked keys, whose k and
+ * v rows are zero) each element's rows saw.  For every row r < rows and head h:
+ * share = npad[b] * exp(-lse), out[b, r, h * 128 + j] = bf16(o[b, h, r, j] /
+ * (1 - share)) (f32, each step correctly rounded, round to nearest even),
+ * out bf16 with row stride ldo >= heads * 128; and *guard (f32, >= 0) is
+ * raised to the largest share (the caller recomputes rows whose share is near
+ * 1, where the division loses precision).  o / out strides multiples of 8,
+ * o / out 16-byte aligned.  No counterpart in the reference, whose attention
+ * runs over the real keys only: for the DiT step drivers, which pad the joint
+ * sequence to a length the fused attention kernels run fastest at.
+ * Asynchronous on stream. */
+int mq_attn_pad_correct(const void *o, int64_t batch, int heads, int64_t rows, int64_t o_batch_stride,
+                        int64_t o_head_stride, int64_t o_row_stride, const float *lse, int64_t lse_batch_stride,
+                        int64_t lse_head_stride, const float *npad, void *out, int64_t out_batch_stride, int64_t ldo,
+                        float *guard, void *stream);
+
 /* Quantize activations once for several Q4_K GEMVs: x [m, k] (F32 or BF16,
  * row stride ldx, 16-byte aligned rows) -> m * k / 256 blocks of
  * MQ_X_Q8K_BLOCK_BYTES at dst (16-byte aligned), by the Q8_K quantization

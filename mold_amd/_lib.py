@@ -48,6 +48,8 @@ SIGNATURES = {
     "mq_gelu_tanh_bf16": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "mq_qk_norm_rope": (_int, [_vp, _int, _i64, _i64, _int, _int, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp,
                                _vp, _i64, _i64, _vp]),
+    "mq_attn_pad_correct": (_int, [_vp, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64, _i64,
+                                   _vp, _vp]),
     "mq_gguf_open": (_int, [ctypes.c_char_p, _pp]),
     "mq_gguf_close": (None, [_vp]),
     "mq_gguf_tensor_count": (_i64, [_vp]),

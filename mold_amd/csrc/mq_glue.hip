@@ -14,6 +14,10 @@
 //     [heads, L, 128] at a row offset of a joint sequence: what the qkv
 //     projection output goes through before attention (FLUX offload.rs:
 //     188-201 and :56-66; Qwen-Image quantized_transformer.rs:739-751).
+//   * mq_attn_pad_correct: the output of an attention run over zero-padded
+//     keys, rescaled per (row, head) to the softmax over the real keys from
+//     the log-sum-exp the attention kernel returns, and written in the
+//     [rows, heads * 128] layout the out-projection reads.
 //
 // All are HBM-bound (f32 or bf16 in, bf16 out, a few flops per byte).
 #include "../../include/moldq.h"
@@ -152,6 +156,59 @@ __global__ __launch_bounds__(256) void gelu_bf16_kernel(const IN *__restrict__ s
   }
 }
 
+// Zero-padded attention: the n zero keys a row of batch element b saw add
+// exp(0) = 1 each to its softmax denominator and nothing to the numerator, so
+// the output over the real keys is o / s with s = 1 - n exp(-lse), lse the
+// row's log-sum-exp over all keys.  Thread t takes the 8 bf16 (16 bytes) of
+// chunk c = t % 16 of head h of row r of element b (t = ((b * rows + r) *
+// heads + h) * 16 + c, grid-stride): its loads and stores are whole 256-byte
+// head rows.  Arithmetic in f32 in the order share = n * exp(-lse), inv =
+// 1 / (1 - share), bf16(o * inv) (round to nearest even), each step one
+// correctly rounded f32 operation.  guard (f32 bits, never negative) is
+// raised to the largest share seen: a block's maximum, one atomic max on the
+// bits per block whose maximum exceeds the value it read (a NaN share sticks,
+// as a NaN would through a max that propagates it).
+__global__ __launch_bounds__(256) void attn_pad_correct_kernel(
+    const __bf16 *__restrict__ o, int64_t sob, int64_t soh, int64_t sor, const float *__restrict__ lse, int64_t slb,
+    int64_t slh, const float *__restrict__ npad, int heads, int64_t rows, int64_t items, __bf16 *__restrict__ out,
+    int64_t sb_out, int64_t ldo, unsigned int *__restrict__ guard) {
+#pragma clang fp contract(off)  // share, 1 - share and the product each rounded, as written
+  __shared__ float red[4];
+  float smax = 0.f;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < items; t += (int64_t)gridDim.x * 256) {
+    const int c = (int)(t & 15);
+    const uint32_t rh = (uint32_t)(t >> 4);  // (b * rows + r) * heads + h < 2^31 (checked by the host)
+    const uint32_t br = rh / (uint32_t)heads;
+    const int h = (int)(rh - br * (uint32_t)heads);
+    const uint32_t b = br / (uint32_t)rows, r = br - b * (uint32_t)rows;
+    const float share = npad[b] * expf(-lse[(int64_t)b * slb + h * slh + r]);
+    const float inv = 1.0f / (1.0f - share);
+    smax = (share > smax || share != share) ? share : smax;
+    const uint4 v = *reinterpret_cast<const uint4 *>(o + (int64_t)b * sob + h * soh + (int64_t)r * sor + 8 * c);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      p[i] = pack_bf16x2(__uint_as_float(w[i] << 16) * inv, __uint_as_float(w[i] & 0xFFFF0000u) * inv);
+    *reinterpret_cast<uint4 *>(out + (int64_t)b * sb_out + (int64_t)r * ldo + (int64_t)h * kHead + 8 * c) =
+        make_uint4(p[0], p[1], p[2], p[3]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float u = __shfl_xor(smax, off);
+    smax = (u > smax || u != u) ? u : smax;
+  }
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = smax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < 4; ++i) m = (red[i] > m || red[i] != red[i]) ? red[i] : m;
+    const unsigned int bits = __float_as_uint(m);
+    if (bits > __hip_atomic_load(guard, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(guard, bits);
+  }
+}
+
 int invalid(const char *msg) { return set_error(MQ_E_INVALID, msg); }
 
 bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -222,6 +279,33 @@ int mq_gelu_tanh_bf16(const void *src, int src_dtype, int64_t rows, int64_t cols
   else
     hipLaunchKernelGGL(gelu_bf16_kernel<__bf16>, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const __bf16 *>(src), rows, cols4, lds, static_cast<uint2 *>(dst), ldd / 4);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
+}
+
+int mq_attn_pad_correct(const void *o, int64_t batch, int heads, int64_t rows, int64_t o_batch_stride,
+                        int64_t o_head_stride, int64_t o_row_stride, const float *lse, int64_t lse_batch_stride,
+                        int64_t lse_head_stride, const float *npad, void *out, int64_t out_batch_stride, int64_t ldo,
+                        float *guard, void *stream) {
+  if (batch < 0 || rows < 0 || heads <= 0) return invalid("mq_attn_pad_correct: negative batch or rows, or heads < 1");
+  if (!o || !lse || !npad || !out || !guard) return invalid("mq_attn_pad_correct: NULL pointer");
+  if (o_batch_stride < 0 || o_head_stride < 0 || o_row_stride < 0 || lse_batch_stride < 0 || lse_head_stride < 0 ||
+      out_batch_stride < 0 || ldo < (int64_t)heads * kHead)
+    return invalid("mq_attn_pad_correct: negative stride, or ldo < heads * 128");
+  if (o_batch_stride % 8 || o_head_stride % 8 || o_row_stride % 8 || out_batch_stride % 8 || ldo % 8)
+    return invalid("mq_attn_pad_correct: o and out strides must be multiples of 8 elements");
+  if (!aligned(o, 16) || !aligned(out, 16) || !aligned(lse, 4) || !aligned(npad, 4) || !aligned(guard, 4))
+    return invalid("mq_attn_pad_correct: misaligned buffer");
+  if (batch * rows * (int64_t)heads >= (int64_t(1) << 31))
+    return invalid("mq_attn_pad_correct: batch * rows * heads must be below 2^31");
+  const int64_t items = batch * rows * heads * (kHead / 8);
+  if (items == 0) return MQ_OK;
+  const int64_t blocks = (items + 255) / 256;
+  const dim3 grid((unsigned)(blocks < 4096 ? blocks : 4096));
+  hipLaunchKernelGGL(attn_pad_correct_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const __bf16 *>(o), o_batch_stride, o_head_stride, o_row_stride, lse,
+                     lse_batch_stride, lse_head_stride, npad, heads, rows, items, static_cast<__bf16 *>(out),
+                     out_batch_stride, ldo, reinterpret_cast<unsigned int *>(guard));
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MQ_OK : set_error(MQ_E_HIP, hipGetErrorString(e));
 }

@@ -385,20 +385,26 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
             if valid < l or n_drop:
                 o_pad, lse = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None],
                                                                                     None, True)[:2]
+                if guard is not None:
+                    # one fused pass (libmoldq): the share, the f32 correction, bf16, the
+                    # [valid, h*d] layout and the guard
+                    from .fused import attn_pad_correct
+                    res = (out if out is not None
+                           else torch.empty((valid, h * d), dtype=torch.bfloat16, device=q.device))
+                    attn_pad_correct(o_pad, lse, _npad(q.device, (l - valid + n_drop,)), valid, guard, res)
+                    ATTENTION_BACKEND["name"] = "fused"
+                    return res
                 pad_share = (l - valid + n_drop) * torch.exp(-lse[0, :, :valid])  # [h, valid] f32, 1 - s
                 # one pass: correct in f32, round to bf16, write the [valid, h, d] layout
                 res = (out.view(valid, h, d) if out is not None
                        else torch.empty((valid, h, d), dtype=torch.bfloat16, device=q.device))
                 torch.mul(o_pad[0, :, :valid].transpose(0, 1), (1.0 / (1.0 - pad_share)).transpose(0, 1)[..., None],
                           out=res)
-                if guard is not None:
-                    torch.maximum(guard, pad_share.amax(), out=guard)
-                else:
-                    bad = (pad_share > 1.0 - PAD_MIN_SHARE).any(dim=1)
-                    if bool(bad.any()):
-                        heads = bad.nonzero().flatten()
-                        exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid], drop)
-                        res[:, heads] = exact.view(valid, heads.numel(), d)
+                bad = (pad_share > 1.0 - PAD_MIN_SHARE).any(dim=1)
+                if bool(bad.any()):
+                    heads = bad.nonzero().flatten()
+                    exact = _attention_chunked(qb[heads, :valid], kb[heads, :valid], vb[heads, :valid], drop)
+                    res[:, heads] = exact.view(valid, heads.numel(), d)
                 ATTENTION_BACKEND["name"] = "fused"
                 return out if out is not None else res.reshape(valid, h * d)
             else:
@@ -421,6 +427,18 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
 
 
 _NPAD_CACHE: dict = {}
+
+
+def _npad(device, counts):
+    """f32 [len(counts)] device tensor of the zero-key counts, uploaded once per
+    distinct padding (not per call)."""
+    import torch
+    key = (device, tuple(counts))
+    t = _NPAD_CACHE.get(key)
+    if t is None:
+        t = torch.tensor(counts, dtype=torch.float32, device=device)
+        _NPAD_CACHE[key] = t
+    return t
 
 
 def attention_bf16_batch(q, k, v, valid: int, guard, drops):
@@ -446,17 +464,11 @@ def attention_bf16_batch(q, k, v, valid: int, guard, drops):
         ATTENTION_BACKEND["name"] = "chunked"
         return per_element()
     counts = tuple(l - valid + (0 if dr is None else max(0, dr[1] - dr[0])) for dr in drops)
-    key = (q.device, counts)
-    npad = _NPAD_CACHE.get(key)
-    if npad is None:   # one small upload per distinct padding, not per call
-        npad = torch.tensor(counts, dtype=torch.float32, device=q.device).view(b_, 1, 1)
-        _NPAD_CACHE[key] = npad
-    pad_share = npad * torch.exp(-lse[:, :, :valid])          # [B, h, valid] f32, 1 - s
-    res = torch.empty((b_, valid, h, d), dtype=torch.bfloat16, device=q.device)
-    torch.mul(out[:, :, :valid].transpose(1, 2), (1.0 / (1.0 - pad_share)).transpose(1, 2)[..., None], out=res)
-    torch.maximum(guard, pad_share.amax(), out=guard)
+    from .fused import attn_pad_correct
+    res = torch.empty((b_, valid, h * d), dtype=torch.bfloat16, device=q.device)
+    attn_pad_correct(out, lse, _npad(q.device, counts), valid, guard, res)
     ATTENTION_BACKEND["name"] = "fused"
-    return res.reshape(b_, valid, h * d)
+    return res
 
 
 def attention_f32(q, k, v):

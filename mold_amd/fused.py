@@ -1,5 +1,6 @@
 """Fused block glue on the device: libmoldq's row passes between the quantized
-linears (mq_adaln_modulate, mq_gelu_tanh_bf16, mq_qk_norm_rope in include/moldq.h).
+linears (mq_adaln_modulate, mq_gelu_tanh_bf16, mq_qk_norm_rope and
+mq_attn_pad_correct in include/moldq.h).
 
 All run on torch's current stream and allocate only their outputs.  They need
 the HIP library (no fallback); the host-CPU path of the block graphs keeps the
@@ -53,11 +54,43 @@ def new_heads(heads: int, l_total: int, device, valid=None, batch=None):
     sequence) are zero, rows before it are left for qk_norm_rope to fill."""
     import torch
     shape = (heads, l_total, HEAD_DIM) if batch is None else (batch, heads, l_total, HEAD_DIM)
-    bufs = tuple(torch.empty(shape, dtype=torch.bfloat16, device=device) for _ in range(3))
+    # one allocation, so that the padding rows of all three clear in one launch
+    qkv = torch.empty((3,) + shape, dtype=torch.bfloat16, device=device)
     if valid is not None and valid < l_total:
-        for t in bufs:
-            t[..., valid:, :].zero_()
-    return bufs
+        qkv[..., valid:, :].zero_()
+    return qkv[0], qkv[1], qkv[2]
+
+
+def attn_pad_correct(o, lse, npad, rows: int, guard, out):
+    """Rows 0 .. rows-1 of an attention computed over zero-padded keys, corrected
+    to the softmax over the real keys: out[b, r, h*128 + j] = bf16(o[b, h, r, j]
+    / (1 - npad[b] exp(-lse[b, h, r]))), and guard (0-dim f32) raised to the
+    largest npad exp(-lse) (mq_attn_pad_correct).  o bf16 [B, H, >= rows, 128]
+    with unit stride along the head dim; lse f32 [B, H, >= rows] with unit
+    stride along rows; npad f32 [B] (contiguous); out bf16 [B, rows, H*128] or,
+    for B = 1, [rows, H*128], unit column stride."""
+    import torch
+    if o.dtype != torch.bfloat16 or o.dim() != 4 or o.shape[3] != HEAD_DIM or o.stride(3) != 1 or o.shape[2] < rows:
+        raise ValueError("attn_pad_correct: o must be bf16 [B, H, >= rows, 128] with unit stride along the head dim")
+    b_, h = o.shape[0], o.shape[1]
+    if lse.dtype != torch.float32 or lse.dim() != 3 or tuple(lse.shape[:2]) != (b_, h) or lse.shape[2] < rows \
+            or lse.stride(2) != 1:
+        raise ValueError("attn_pad_correct: lse must be f32 [B, H, >= rows] with unit stride along rows")
+    if npad.dtype != torch.float32 or not npad.is_contiguous() or npad.numel() != b_:
+        raise ValueError("attn_pad_correct: npad must be contiguous f32 [B]")
+    if guard.dtype != torch.float32 or guard.numel() != 1:
+        raise ValueError("attn_pad_correct: guard must be a one-element f32 tensor")
+    o3 = out if out.dim() == 3 else out.unsqueeze(0)
+    if out.dtype != torch.bfloat16 or tuple(o3.shape) != (b_, rows, h * HEAD_DIM) or o3.stride(2) != 1:
+        raise ValueError("attn_pad_correct: out must be bf16 [B, rows, H*128] with unit column stride")
+    for t in (o, lse, npad, guard, out):
+        if t.device != o.device:
+            raise ValueError("attn_pad_correct: every tensor must be on o's device")
+    check(_lib.load().mq_attn_pad_correct(o.data_ptr(), b_, h, rows, o.stride(0), o.stride(1), o.stride(2),
+                                          lse.data_ptr(), lse.stride(0), lse.stride(1), npad.data_ptr(),
+                                          out.data_ptr(), o3.stride(0), o3.stride(1), guard.data_ptr(),
+                                          _stream_ptr()))
+    return out
 
 
 def qk_norm_rope(qkv, heads: int, q_weight, k_weight, cos, sin, q_out, k_out, v_out, row_off: int,

@@ -1,12 +1,16 @@
-"""GPU tests of libmoldq's fused block glue (mq_adaln_modulate, mq_qk_norm_rope)
-against f64 torch restatements of the ops they replace:
+"""GPU tests of libmoldq's fused block glue (mq_adaln_modulate, mq_qk_norm_rope,
+mq_gelu_tanh_bf16, mq_attn_pad_correct) against torch restatements of the ops they
+replace:
   modulate   LayerNorm(eps 1e-6, no affine) * (1 + scale) + shift, to bf16
              (crates/mold-inference/src/flux/offload.rs:75-78, 283-286)
   qk norm    x / sqrt(mean(x^2) + eps) * w for q and k per head (offload.rs:160-167, 188-201)
   RoPE       pair (2i, 2i+1) rotated by angle i: (c x0 - s x1, s x0 + c x1) (offload.rs:56-66)
+  pad fix    o / (1 - n exp(-lse)) per (row, head) of an attention over n zero keys
 The kernels compute in f32 and round once to bf16, so every output must lie within
 one bf16 ulp of the f64 value (half an ulp of rounding plus f32 noise), and v, a
-plain bf16 conversion, must equal torch's conversion bit for bit.
+plain bf16 conversion, must equal torch's conversion bit for bit.  The padded
+attention's correction repeats torch's f32 op sequence (exp, multiply, subtract,
+reciprocal, multiply, round), so it must equal that sequence bit for bit.
 """
 import numpy as np
 import pytest
@@ -244,6 +248,62 @@ def test_padded_attention_guard_and_step_rerun():
     assert st.calls == [True, False] and st.pad_attention and st._guard is None
     err = ((out.double().cpu() - ref).norm() / ref.norm()).item()
     assert err < 5e-3, err
+
+
+@pytest.mark.parametrize("B,H,rows,L,layout", [(1, 24, 7145, 7168, "bhld"), (2, 4, 700, 768, "blhd"),
+                                                (1, 3, 5, 64, "bhld"), (2, 2, 1, 32, "blhd")])
+def test_attn_pad_correct_matches_torch_sequence(B, H, rows, L, layout):
+    """mq_attn_pad_correct against the torch ops it replaces in the padded attention:
+    share = n_b * exp(-lse), out = bf16(o * (1 / (1 - share))) in the [rows, H*128]
+    layout, guard = max(guard, max share).  o in the attention's [B, H, L, 128] view
+    over head-major or row-major memory; out also as a column block of a wider buffer."""
+    print(f"[case] attn_pad_correct B={B} H={H} rows={rows} L={L} {layout}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(rows + 7 * B)
+    if layout == "bhld":
+        o = torch.randn((B, H, L, 128), device="cuda", generator=g).to(torch.bfloat16)
+    else:
+        o = torch.randn((B, L, H, 128), device="cuda", generator=g).to(torch.bfloat16).transpose(1, 2)
+    lse = (float(np.log(L)) + 2.0 * torch.randn((B, H, L + 5), device="cuda", generator=g))[:, :, :L]
+    counts = [L - rows + 3 * b for b in range(B)]
+    npad = torch.tensor(counts, dtype=torch.float32, device="cuda")
+    share = npad.view(B, 1, 1) * torch.exp(-lse[:, :, :rows])
+    ref = torch.empty((B, rows, H, 128), dtype=torch.bfloat16, device="cuda")
+    torch.mul(o[:, :, :rows].transpose(1, 2), (1.0 / (1.0 - share)).transpose(1, 2)[..., None], out=ref)
+    ref = ref.reshape(B, rows, H * 128)
+    guard = torch.zeros((), dtype=torch.float32, device="cuda")
+    out = FU.attn_pad_correct(o, lse, npad, rows, guard, torch.empty_like(ref))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert float(guard) == float(share.amax())
+    big = torch.full((), 1e3, dtype=torch.float32, device="cuda")    # the guard is only raised
+    FU.attn_pad_correct(o, lse, npad, rows, big, out)
+    assert float(big) == 1e3
+    buf = torch.full((B, rows, H * 128 + 48), 7.0, dtype=torch.bfloat16, device="cuda")
+    FU.attn_pad_correct(o, lse, npad, rows, guard, buf[:, :, 16:16 + H * 128])
+    torch.cuda.synchronize()
+    assert torch.equal(buf[:, :, 16:16 + H * 128], ref)
+    assert bool((buf[:, :, :16] == 7.0).all()) and bool((buf[:, :, 16 + H * 128:] == 7.0).all())
+
+
+def test_attn_pad_correct_errors_are_reported():
+    o = torch.zeros((1, 2, 8, 128), dtype=torch.bfloat16, device="cuda")
+    lse = torch.zeros((1, 2, 8), device="cuda")
+    npad = torch.ones(1, device="cuda")
+    guard = torch.zeros((), device="cuda")
+    out = torch.empty((1, 4, 256), dtype=torch.bfloat16, device="cuda")
+    lib = mold_amd.load()
+    rc = lib.mq_attn_pad_correct(o.data_ptr(), 1, 2, 4, o.stride(0), o.stride(1), o.stride(2), lse.data_ptr(),
+                                 lse.stride(0), lse.stride(1), npad.data_ptr(), out.data_ptr(), out.stride(0), 200,
+                                 guard.data_ptr(), None)
+    assert rc == -1 and b"ldo" in lib.mq_last_error()
+    rc = lib.mq_attn_pad_correct(o.data_ptr(), 1, 2, 4, o.stride(0), o.stride(1), 132, lse.data_ptr(),
+                                 lse.stride(0), lse.stride(1), npad.data_ptr(), out.data_ptr(), out.stride(0), 256,
+                                 guard.data_ptr(), None)
+    assert rc == -1 and b"multiples of 8" in lib.mq_last_error()
+    with pytest.raises(ValueError):   # more rows than o holds
+        FU.attn_pad_correct(o, lse, npad, 9, guard, torch.empty((1, 9, 256), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError):   # lse of the wrong head count
+        FU.attn_pad_correct(o, lse[:, :1], npad, 4, guard, out)
 
 
 def test_glue_errors_are_reported():
