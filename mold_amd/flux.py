@@ -373,7 +373,6 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
     head-chunked path on the valid rows (any other error propagates).  The
     backend used is recorded in ATTENTION_BACKEND."""
     import torch
-    from torch.nn.attention import SDPBackend, sdpa_kernel
     h, l, d = q.shape
     valid = l if valid is None else valid
     qb, kb, vb = (t.to(torch.bfloat16).contiguous() for t in (q, k, v))
@@ -408,8 +407,13 @@ def attention_bf16(q, k, v, valid: Optional[int] = None, guard=None, drop: Optio
                 ATTENTION_BACKEND["name"] = "fused"
                 return out if out is not None else res.reshape(valid, h * d)
             else:
-                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                    o = torch.nn.functional.scaled_dot_product_attention(qb[None], kb[None], vb[None])[0]
+                # the memory-efficient entry: its output is laid out token-major ([L, H, D]
+                # under the [H, L, D] view), so the [L, H*D] result below is a view, and it
+                # runs faster than the flash entry at these shapes (24 x 4608 x 128 on an
+                # MI355X: 504 vs 541 us, identical values, and flash's head-major output
+                # needed a 21.5 us transposing copy)
+                o = torch.ops.aten._scaled_dot_product_efficient_attention(qb[None], kb[None], vb[None], None,
+                                                                           False)[0][0]
             ATTENTION_BACKEND["name"] = "fused"
             if out is not None:
                 out.view(valid, h, d).copy_(o.transpose(0, 1))
