@@ -193,6 +193,17 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype,
                int64_t m, int64_t ldx, void *y, int y_dtype, int64_t ldy,
                const float *bias, int act, void *stream);
 
+/* mq_qmatmul with the activation applied to output columns act_col0 .. n-1
+ * only (0 <= act_col0 <= n; 0 is mq_qmatmul, n applies none): columns before
+ * act_col0 are x . W^T + bias as computed by mq_qmatmul without act, columns
+ * from act_col0 on as computed with it, bit for bit.  No counterpart in
+ * candle: for the FLUX single block, whose linear1 output is split into the
+ * attention's q, k, v and the MLP half that goes through gelu() before
+ * linear2 (crates/mold-inference/src/flux/offload.rs:380-394); with the GELU
+ * in linear1's epilogue the MLP half is linear2's input as it stands. */
+int mq_qmatmul_act_from(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
+                        int y_dtype, int64_t ldy, const float *bias, int act, int64_t act_col0, void *stream);
+
 /* mq_qmatmul that allocates nothing, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  Same arguments,

@@ -41,6 +41,7 @@ SIGNATURES = {
                                ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "mq_dequantize": (_int, [_vp, _vp, _vp, _int, _vp]),
     "mq_qmatmul": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _int, _i64, _vp, _int, _vp]),
+    "mq_qmatmul_act_from": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _int, _i64, _vp, _int, _i64, _vp]),
     "mq_quantize_x_q8k": (_int, [_vp, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
     "mq_qmatmul_noalloc": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _int, _i64, _vp, _int, _vp]),
     "mq_qmatmul_gated_add": (_int, [_vp, _vp, _vp, _int, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),

@@ -837,9 +837,11 @@ int mq_qmatmul_workspace_size(mq_ctx *ctx, const mq_qtensor *w, int x_dtype, int
   return MQ_OK;
 }
 
-int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
-               int y_dtype, int64_t ldy, const float *bias, int act, void *stream) {
-  int rc = check_qmatmul_args("mq_qmatmul", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
+// mq_qmatmul with the activation on output columns act_col0 .. n-1 only.
+static int qmatmul_cols(const char *fn, mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m,
+                        int64_t ldx, void *y, int y_dtype, int64_t ldy, const float *bias, int act, int64_t act_col0,
+                        void *stream) {
+  int rc = check_qmatmul_args(fn, ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, act);
   if (rc || m == 0) return rc;
   DeviceGuard g(ctx->device);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -849,7 +851,22 @@ int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int
     rc = stream_workspace(ctx, s, p.total, &ws);
     if (rc) return rc;
   }
-  return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act, s);
+  return run_qmatmul(ctx, w, p, ws, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, nullptr, act_code(act, act_col0), s);
+}
+
+int mq_qmatmul(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
+               int y_dtype, int64_t ldy, const float *bias, int act, void *stream) {
+  return qmatmul_cols("mq_qmatmul", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, act, 0, stream);
+}
+
+int mq_qmatmul_act_from(mq_ctx *ctx, const mq_qtensor *w, const void *x, int x_dtype, int64_t m, int64_t ldx, void *y,
+                        int y_dtype, int64_t ldy, const float *bias, int act, int64_t act_col0, void *stream) {
+  if (!w) return fail(MQ_E_INVALID, "mq_qmatmul_act_from: NULL weight");
+  if (act_col0 < 0 || act_col0 > w->n || w->n >= (int64_t(1) << 30))
+    return fail(MQ_E_INVALID, "mq_qmatmul_act_from: act_col0=%lld outside 0 .. n=%lld (n below 2^30)",
+                (long long)act_col0, (long long)w->n);
+  return qmatmul_cols("mq_qmatmul_act_from", ctx, w, x, x_dtype, m, ldx, y, y_dtype, ldy, bias, act, act_col0,
+                      stream);
 }
 
 int mq_quantize_x_q8k(mq_ctx *ctx, const void *x, int x_dtype, int64_t m, int64_t k, int64_t ldx, void *dst,

@@ -215,7 +215,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void gemm_kernel(
       for (int e = 0; e < 16; ++e) {
         const int64_t row = m0 + mb * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
         if (row < m)
-          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, act_out<OUT>(acc[mb][nb][e] + bv, act), gate, g);
+          store_epi<OUT>(y + row * ldy + col, res + row * ldy + col, act_out<OUT>(acc[mb][nb][e] + bv, act_at(act, col)),
+                         gate, g);
       }
     }
   }
@@ -398,6 +399,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
   const int64_t col = c0 + l32;
   const int64_t row0 = m0 + 4 * h;
   const bool colok = col < n;
+  const int la = act_at(act, col);  // this lane's column's activation
   const float bv = bias && colok ? bias[col] : 0.f;
   OUT *yc = y + row0 * ldy + col;
   if constexpr (GATED) {
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
     // rows past m and columns past n are neither read nor written
     const float g = colok ? gate[col] : 0.f;
     float r[2][16];
-    if (m0 + kFM <= m && c0 + 32 <= n && act == MQ_ACT_NONE_) {
+    if (m0 + kFM <= m && c0 + 32 <= n && la == MQ_ACT_NONE_) {
       // whole tile, no activation (every gated linear of the block graphs):
       // no bounds checks
       auto load_full = [&](int mb, float *dst) {
@@ -440,7 +442,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
-        if (colok && row0 + ro < m) yc[ro * ldy] = __builtin_fmaf(g, act_out<float>(acc[mb][e] + bv, act), r[mb & 1][e]);
+        if (colok && row0 + ro < m) yc[ro * ldy] = __builtin_fmaf(g, act_out<float>(acc[mb][e] + bv, la), r[mb & 1][e]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
   } else {
     if (m0 + kFM <= m && c0 + 32 <= n) {
       // whole tile: no row checks, the activation chosen once
-      if (act == MQ_ACT_NONE_) {
+      if (la == MQ_ACT_NONE_) {
 #pragma unroll
         for (int mb = 0; mb < kMB; ++mb)
 #pragma unroll
@@ -469,7 +471,7 @@ __global__ __launch_bounds__(64 * kW, 8 / kW) void gemm_fast_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int64_t ro = mb * 32 + 8 * (e >> 2) + (e & 3);
-        if (row0 + ro < m) store_out<OUT>(yc + ro * ldy, act_out<OUT>(acc[mb][e] + bv, act));
+        if (row0 + ro < m) store_out<OUT>(yc + ro * ldy, act_out<OUT>(acc[mb][e] + bv, la));
       }
   }
 }
@@ -515,10 +517,10 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
     // vector access each
     float o[4];
     const float4 bv = bias ? *reinterpret_cast<const float4 *>(bias + col0) : make_float4(0.f, 0.f, 0.f, 0.f);
-    o[0] = act_out<OUT>(sv[0] + bv.x, act);
-    o[1] = act_out<OUT>(sv[1] + bv.y, act);
-    o[2] = act_out<OUT>(sv[2] + bv.z, act);
-    o[3] = act_out<OUT>(sv[3] + bv.w, act);
+    o[0] = act_out<OUT>(sv[0] + bv.x, act_at(act, col0));
+    o[1] = act_out<OUT>(sv[1] + bv.y, act_at(act, col0 + 1));
+    o[2] = act_out<OUT>(sv[2] + bv.z, act_at(act, col0 + 2));
+    o[3] = act_out<OUT>(sv[3] + bv.w, act_at(act, col0 + 3));
     if constexpr (std::is_same_v<OUT, float>) {
       float4 *yv = reinterpret_cast<float4 *>(yr);
       if (gate) {
@@ -544,13 +546,14 @@ __global__ __launch_bounds__(256) void gemm_tail_reduce_kernel(const float *__re
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (col0 + j < n)
-          yr[j] = __builtin_fmaf(gate[col0 + j], act_out<float>(sv[j] + (bias ? bias[col0 + j] : 0.f), act), rv[j]);
+          yr[j] = __builtin_fmaf(gate[col0 + j], act_out<float>(sv[j] + (bias ? bias[col0 + j] : 0.f), act_at(act, col0 + j)),
+                                 rv[j]);
       return;
     }
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act));
+    if (col0 + j < n) store_out<OUT>(yr + j, act_out<OUT>(sv[j] + (bias ? bias[col0 + j] : 0.f), act_at(act, col0 + j)));
 }
 
 template <typename OUT, bool GATED, int FM, int W>

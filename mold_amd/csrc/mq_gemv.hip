@@ -91,7 +91,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     if (row < n) {
       if (ksplit == 1) {
         if (bias) s += bias[row];
-        store1<OUT>(y + m * ldy + row, apply_act(s, act));
+        store1<OUT>(y + m * ldy + row, apply_act(s, act_at(act, row)));
       } else {
         partial[((int64_t)ks * M + m) * npad + row] = s;
       }
@@ -109,7 +109,7 @@ __global__ void gemv_reduce_kernel(const float *__restrict__ partial, int ksplit
   float s = 0.f;
   for (int ks = 0; ks < ksplit; ++ks) s += partial[((int64_t)ks * m + mm) * npad + row];
   if (bias) s += bias[row];
-  store1<OUT>(y + mm * ldy + row, apply_act(s, act));
+  store1<OUT>(y + mm * ldy + row, apply_act(s, act_at(act, row)));
 }
 
 // ---------------------------------------------------------------------------
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(kQ4kThreads) void gemv_q4k_kernel(
     float acc = 0.f;
     for (int sb = 0; sb < nb; ++sb) acc += red[(sb * rows + rl) * M + m];
     if (bias) acc += bias[row];
-    store1<OUT>(y + m * ldy + row, apply_act(acc, act));
+    store1<OUT>(y + m * ldy + row, apply_act(acc, act_at(act, row)));
   }
 }
 
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(kFragThreads) void gemv_frag_kernel(WView w, int64_
     float acc = 0.f;
     for (int uh = 0; uh < 2 * units; ++uh) acc += red[(uh * rows + rl) * M + m];
     if (bias) acc += bias[row];
-    store1<OUT>(y + m * ldy + row, apply_act(acc, act));
+    store1<OUT>(y + m * ldy + row, apply_act(acc, act_at(act, row)));
   }
 }
 

@@ -111,6 +111,13 @@ hipError_t launch_gemm_type(const WView &w, int64_t n, int64_t k, int64_t ntiles
                             int64_t lda, void *y, int y_type, int64_t ldy, const float *bias, const float *gate,
                             int act, const GemmTail &tail, float *partial, hipStream_t stream);
 
+// The launchers' `act` argument: bit 0 the activation (MQ_ACT_NONE or
+// MQ_ACT_GELU_TANH), bits 1 and up the first output column it applies to (0
+// for the whole output; mq_qmatmul_act_from sets it).  act_at gives output
+// column col's activation.
+inline int act_code(int act, int64_t first_col) { return act | (int)(first_col << 1); }
+__host__ __device__ __forceinline__ int act_at(int code, int64_t col) { return col >= (code >> 1) ? (code & 1) : 0; }
+
 // Epilogue activation (GELU with the tanh approximation, as candle's gelu()).
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == 1) {

@@ -689,10 +689,21 @@ class FluxStep:
         cfg = self.cfg
         p = f"single_blocks.{i}."
         shift, scale, gate = self._mod(p + "modulation.lin", vec, 3)
+        L, h = x.shape[0], cfg.hidden_size
+        if self._fused(x) and self.bf16_projections and self.gemm_dtype == torch.bfloat16:
+            # linear1 in bf16 with GELU on its MLP columns only (mq_qmatmul_act_from): y =
+            # [q | k | v | gelu(mlp)].  The norm/RoPE pass copies q, k, v into the joint
+            # buffers, after which attention writes its rows over the v columns, so that
+            # y[:, 2h:] = [attention | gelu(mlp)] is linear2's input as it stands (no GELU
+            # pass, no concatenation buffer)
+            y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=torch.bfloat16,
+                                                  act=ACT_GELU_TANH, act_from=3 * h)
+            heads = self._heads_fused([(y, p + "norm.query_norm.scale", p + "norm.key_norm.scale")], cos, sin)
+            self._attn_padded(*heads, L, out=y[:, 2 * h:3 * h])
+            return self._gated(p + "linear2", y[:, 2 * h:], gate, x)
         # on the fused path linear1's output feeds only the norm/RoPE and GELU passes: bf16
         y_dtype = torch.bfloat16 if self._fused(x) and self.bf16_projections else torch.float32
         y = self.p.lin[p + "linear1"].forward(self._modulate(x, shift, scale), out_dtype=y_dtype)
-        L, h = x.shape[0], cfg.hidden_size
         cat = torch.empty((L, h + cfg.mlp_size), dtype=self.gemm_dtype, device=x.device)
         if self._fused(x):
             # attention writes its rows straight into linear2's concatenated input

@@ -244,9 +244,21 @@ class QMatMul:
                                                     ctypes.byref(out)))
         return out.value
 
-    def forward(self, x, bias=None, act: int = ACT_NONE, out_dtype=None, out=None, stream=None):
+    def forward(self, x, bias=None, act: int = ACT_NONE, out_dtype=None, out=None, stream=None, act_from: int = 0):
+        """y = act(x . W^T + bias); with act_from > 0 the activation applies to output
+        columns act_from .. n-1 only (mq_qmatmul_act_from)."""
         torch = _torch()
         n, k = self.w.shape
+        if not 0 <= act_from <= n:
+            raise ValueError(f"QMatMul: act_from {act_from} outside 0 .. {n}")
+
+        def call(xp, xt, m, ldx, y, yt, ldy, b):
+            lib = _lib.load()
+            if act_from:
+                return lib.mq_qmatmul_act_from(self.w.device.handle, self.w.handle, xp, xt, m, ldx, y, yt, ldy, b,
+                                               int(act), int(act_from), _stream_ptr(stream))
+            return lib.mq_qmatmul(self.w.device.handle, self.w.handle, xp, xt, m, ldx, y, yt, ldy, b, int(act),
+                                  _stream_ptr(stream))
         if isinstance(x, Q8KActivations):
             if x.k != k:
                 raise ValueError(f"QMatMul: x k {x.k} != weight k {k}")
@@ -256,10 +268,8 @@ class QMatMul:
             assert out.dtype == out_dtype and tuple(out.shape) == (x.m, n)
             if bias is not None:
                 assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == n
-            check(_lib.load().mq_qmatmul(self.w.device.handle, self.w.handle, x.data.data_ptr(), _lib.MQ_X_Q8K, x.m,
-                                         k, out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
-                                         bias.data_ptr() if bias is not None else None, int(act),
-                                         _stream_ptr(stream)))
+            check(call(x.data.data_ptr(), _lib.MQ_X_Q8K, x.m, k, out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
+                       bias.data_ptr() if bias is not None else None))
             return out.reshape(*x.lead, n)
         if x.shape[-1] != k:
             raise ValueError(f"QMatMul: x last dim {x.shape[-1]} != weight k {k}")
@@ -276,9 +286,8 @@ class QMatMul:
             assert out.dtype == out_dtype and tuple(out.shape) == (m, n)
         if bias is not None:
             assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == n
-        check(_lib.load().mq_qmatmul(self.w.device.handle, self.w.handle, x2.data_ptr(), _dtype_code(x2.dtype), m,
-                                     x2.stride(0), out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
-                                     bias.data_ptr() if bias is not None else None, int(act), _stream_ptr(stream)))
+        check(call(x2.data_ptr(), _dtype_code(x2.dtype), m, x2.stride(0), out.data_ptr(), _dtype_code(out_dtype),
+                   out.stride(0), bias.data_ptr() if bias is not None else None))
         return out.reshape(*lead, n)
 
     __call__ = forward
@@ -315,8 +324,8 @@ class Linear:
     def from_arc(cls, weight: QTensor, bias=None) -> "Linear":
         return cls(weight, bias)
 
-    def forward(self, x, act: int = ACT_NONE, out_dtype=None, stream=None):
-        return self.matmul.forward(x, bias=self.bias, act=act, out_dtype=out_dtype, stream=stream)
+    def forward(self, x, act: int = ACT_NONE, out_dtype=None, stream=None, act_from: int = 0):
+        return self.matmul.forward(x, bias=self.bias, act=act, out_dtype=out_dtype, stream=stream, act_from=act_from)
 
     def gated_add(self, x, gate, residual, stream=None):
         """residual += gate * forward(x), in place, fused into the GEMM epilogue

@@ -871,6 +871,40 @@ def test_gemm_tail_tiles_split_k(dev, torch, m, tname, mode):
     assert O.rel_l2(got, ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("m,n,k,tname,out_bf16", [
+    (600, 1024, 512, "Q4_K", True),    # 256 x 256 tiles
+    (2304, 7680, 1024, "Q2_K", False), # a full round plus tail tiles split over K
+    (77, 1024, 1024, "Q8_0", True),    # small-m tiles with the tail split
+    (1, 768, 512, "Q4_K", False),      # Q4_K GEMV
+    (3, 640, 512, "Q6_K", True),       # frag GEMV
+    (6, 640, 512, "Q3_K", False),      # generic GEMV
+])
+def test_qmatmul_act_from_splits_the_epilogue(dev, torch, m, n, k, tname, out_bf16):
+    """mq_qmatmul_act_from: output columns before act_col0 equal mq_qmatmul without the
+    activation, columns from act_col0 on equal mq_qmatmul with GELU, bit for bit, on the GEMM
+    (whole tiles, tail split, small-m tiles) and every GEMV kernel; act_col0 at a tile
+    boundary, inside a wave's 32 columns, and at 0 and n."""
+    t = GgmlDType[tname]
+    _say(f"act_from {tname} m={m} n={n} k={k} bf16={out_bf16}")
+    blocks = _weights(int(t), n, k, seed=n + m)
+    b = torch.from_numpy((np.random.default_rng(5).standard_normal(n) * 0.1).astype(np.float32)).cuda()
+    mm = mold_amd.QMatMul(QTensor.from_blocks(dev, t, (n, k), blocks))
+    x = torch.randn((m, k), device="cuda", generator=torch.Generator(device="cuda").manual_seed(m))
+    od = torch.bfloat16 if out_bf16 else torch.float32
+    plain = mm.forward(x, bias=b, out_dtype=od)
+    gelu = mm.forward(x, bias=b, act=mold_amd.ACT_GELU_TANH, out_dtype=od)
+    for c0 in sorted({256, 100, 0, n}):
+        y = mm.forward(x, bias=b, act=mold_amd.ACT_GELU_TANH, out_dtype=od, act_from=c0)
+        torch.cuda.synchronize()
+        assert torch.equal(y[:, :c0], plain[:, :c0]), c0
+        assert torch.equal(y[:, c0:], gelu[:, c0:]), c0
+    lib = mold_amd.load()
+    y = torch.empty((m, n), device="cuda")
+    rc = lib.mq_qmatmul_act_from(dev.handle, mm.w.handle, x.data_ptr(), 0, m, k, y.data_ptr(), 0, n, None, 1, n + 1,
+                                 None)
+    assert rc == -1 and b"act_col0" in lib.mq_last_error()
+
+
 def test_full_flux_single_block_linear1_q4k(dev, torch):
     _say("full shape Q4_K 4608x3072->21504")
     _sampled_rows_check(dev, torch, GgmlDType.Q4_K, 4608, 21504, 3072, seed=4)
