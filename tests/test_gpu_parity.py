@@ -878,12 +878,13 @@ def test_gemm_tail_tiles_split_k(dev, torch, m, tname, mode):
     (1, 768, 512, "Q4_K", False),      # Q4_K GEMV
     (3, 640, 512, "Q6_K", True),       # frag GEMV
     (6, 640, 512, "Q3_K", False),      # generic GEMV
+    (300, 200, 96, "Q4_0", True),      # generic GEMM (k not a whole unit), edge tiles
 ])
 def test_qmatmul_act_from_splits_the_epilogue(dev, torch, m, n, k, tname, out_bf16):
     """mq_qmatmul_act_from: output columns before act_col0 equal mq_qmatmul without the
     activation, columns from act_col0 on equal mq_qmatmul with GELU, bit for bit, on the GEMM
-    (whole tiles, tail split, small-m tiles) and every GEMV kernel; act_col0 at a tile
-    boundary, inside a wave's 32 columns, and at 0 and n."""
+    (whole tiles, tail split, small-m tiles), the generic GEMM and every GEMV kernel; act_col0
+    at a tile boundary, inside a wave's 32 columns, and at 0 and n."""
     t = GgmlDType[tname]
     _say(f"act_from {tname} m={m} n={n} k={k} bf16={out_bf16}")
     blocks = _weights(int(t), n, k, seed=n + m)
@@ -893,7 +894,7 @@ def test_qmatmul_act_from_splits_the_epilogue(dev, torch, m, n, k, tname, out_bf
     od = torch.bfloat16 if out_bf16 else torch.float32
     plain = mm.forward(x, bias=b, out_dtype=od)
     gelu = mm.forward(x, bias=b, act=mold_amd.ACT_GELU_TANH, out_dtype=od)
-    for c0 in sorted({256, 100, 0, n}):
+    for c0 in sorted({min(256, n), 100, 0, n}):
         y = mm.forward(x, bias=b, act=mold_amd.ACT_GELU_TANH, out_dtype=od, act_from=c0)
         torch.cuda.synchronize()
         assert torch.equal(y[:, :c0], plain[:, :c0]), c0
