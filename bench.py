@@ -24,6 +24,10 @@ Also on the same JSON line:
   * "config3_mlp": BASELINE config 3, the MLP chain fc1 (3072->12288, GELU-tanh
     epilogue, bf16 out) then fc2 (12288->3072, f32 out) on f32 x [4608, 3072],
     for Q4_K, Q4_0 and Q6_K weights;
+  * "flux_single_block": FLUX's single-block linear1 and linear2 as the step runs
+    them: linear1 with bf16 output and GELU on its MLP columns only
+    (mq_qmatmul_act_from), linear2 as the gated residual update reading
+    linear1's output columns 6144.. in place (row stride 21504);
   * "tp8_shards": one GPU's share of FLUX's linear1 (column split, N/8) and linear2
     (row split, largest whole-super-block share, gated) under 8-way tensor
     parallelism, at the real shapes (no collective is run);
@@ -215,6 +219,38 @@ def bench_config1(dev, args):
             "gemm_kernel_frac": round(flop / (kms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "what": "f32 x staged to bf16 + fused Q8_0 GEMM (ms, tflops, frac); the GEMM alone on bf16 x "
                     "(gemm_kernel_*)"}
+
+
+def bench_single_block(dev, args):
+    """FLUX's single-block linears at full size, as FluxStep runs them on its fused path:
+    linear1 Q4_K 3072 -> 21504 on bf16 x with bf16 output and GELU on columns 9216.. only
+    (mq_qmatmul_act_from), then linear2 Q4_K 15360 -> 3072 as the gated residual update whose x
+    is linear1's output columns 6144.. (attention rows over the dead v columns, then the GELU'd
+    MLP half), read in place with row stride 21504."""
+    import torch
+    import mold_amd
+    from mold_amd import GgmlDType
+    from mold_amd.quantized import Linear
+    m, h, mlp = 4608, 3072, 12288
+    log("FLUX single block: linear1 (act_from) + linear2 (gated, strided x)")
+    g = torch.Generator(device="cuda").manual_seed(50)
+    mm1 = mold_amd.QMatMul(make_weight(dev, GgmlDType.Q4_K, 3 * h + mlp, h, seed=51))
+    lin2 = Linear(make_weight(dev, GgmlDType.Q4_K, h, h + mlp, seed=52))
+    x = torch.randn((m, h), device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty((m, 3 * h + mlp), dtype=torch.bfloat16, device="cuda")
+    gate = torch.randn(h, device="cuda", generator=g) * 0.01
+    res = torch.zeros((m, h), device="cuda")
+    steps = max(50, args.steps)
+    _, ms1 = timed(lambda: mm1.forward(x, out=y, act=mold_amd.ACT_GELU_TANH, act_from=3 * h), steps, 5,
+                   prewarm_s=0.2)
+    _, ms2 = timed(lambda: lin2.gated_add(y[:, 2 * h:], gate, res), steps, 5)
+    out = {}
+    for name, n, k, ms in (("linear1_act_from", 3 * h + mlp, h, ms1), ("linear2_gated", h, h + mlp, ms2)):
+        flop = 2.0 * m * n * k
+        out[name] = {"m": m, "n": n, "k": k, "ms": round(ms, 4), "tflops": round(flop / (ms * 1e-3) / 1e12, 1),
+                     "frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    del mm1, lin2, x, y, res
+    return out
 
 
 def bench_tp8_shards(dev, args):
@@ -1015,6 +1051,7 @@ def main():
     if not args.no_extra:
         extra["config1_q8_0"] = bench_config1(dev, args)
         extra["config3_mlp"] = bench_config3(dev, args)
+        extra["flux_single_block"] = bench_single_block(dev, args)
         extra["tp8_shards"] = bench_tp8_shards(dev, args)
         extra["dequant"] = bench_dequant(dev, args)
         extra["dense_bf16_ceiling"] = bench_dense_ceiling(args)
