@@ -60,7 +60,10 @@ Also on the same JSON line:
     the final layer on the CPU, extrapolated x19 / x38 and labelled so); its
     "modulation_stack" is the step's 77 adaLN modulation linears (one
     StackedLinear, 1,056,768 x 3072 Q4_K) as the one GEMV the step runs, timed
-    alone, in GB/s against the HBM peak;
+    alone, in GB/s against the HBM peak; its "graphed" is the same forward
+    captured into a HIP graph and replayed (mold_amd.graphs.GraphedStep), in ms
+    per step, and whether a replay equals the eager output bit for bit (the
+    same for "qwen_step");
   * "qwen_step": one Qwen-Image-shaped denoising-step forward at 1328^2
     (60 dual-stream blocks, 6889 image + 256 text
     tokens, q/k/v Q3_K, MLP Q2_K, out-projections and modulation Q4_K), built
@@ -716,6 +719,24 @@ def bench_stack(stack, ms_list, args):
     return out
 
 
+def bench_graphed(step, inp, n, eager_out):
+    """The same forward captured into a HIP graph (mold_amd.graphs.GraphedStep) and replayed:
+    ms per step (median of n), and whether a replay equals the eager output bit for bit."""
+    import torch
+    from mold_amd.graphs import GraphedStep
+    g = GraphedStep(step, **inp)
+    same = bool(torch.equal(g(**inp), eager_out))
+    times = []
+    for _ in range(n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g(**inp)
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    del g
+    return {"ms": round(sorted(times)[len(times) // 2], 3), "steps_timed": n, "equals_eager": same}
+
+
 def bench_flux(dev, args):
     """One FLUX.1-dev-shaped Q4_K step at 1024^2, eager, ms per step."""
     import torch
@@ -744,9 +765,11 @@ def bench_flux(dev, args):
     lin, attn = F.step_flop(cfg, 4096, 512)
     ms = sorted(times)[len(times) // 2]
     log(f"  step {ms:.2f} ms (median of {n}), attention backend {F.ATTENTION_BACKEND['name']}")
+    graphed = bench_graphed(step, inp, n, out)
+    log(f"  graphed step {graphed['ms']:.2f} ms, equals eager: {graphed['equals_eager']}")
     stack = bench_stack(step._mod_stack, (1,), args)
     res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
-           "modulation_stack": stack,
+           "graphed": graphed, "modulation_stack": stack,
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
            "weight_bytes": params.quantized_bytes(), "attention": F.ATTENTION_BACKEND["name"],
@@ -805,9 +828,11 @@ def bench_qwen(dev, args):
     lin, attn = Q.step_flop(cfg, l_img, 256)
     ms = sorted(times)[len(times) // 2]
     log(f"  step {ms:.2f} ms (median of {n}), attention backend {ATTENTION_BACKEND['name']}")
+    graphed = bench_graphed(step, inp, n, out)
+    log(f"  graphed step {graphed['ms']:.2f} ms, equals eager: {graphed['equals_eager']}")
     stack = bench_stack(step._mod_stack, (1, 2), args)
     res = {"ms": round(ms, 3), "steps_timed": n, "all_ms": [round(t, 3) for t in times],
-           "modulation_stack": stack,
+           "graphed": graphed, "modulation_stack": stack,
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
            "cfg_batch2_ms": round(bms, 3), "cfg_batch2_steps_timed": len(btimes),
