@@ -70,7 +70,8 @@ Also on the same JSON line:
     by mold_amd.qwen_image, in ms per step, with a host-CPU baseline (stems,
     block 0 and the output layer on the CPU, extrapolated x60), and the
     batch-2 classifier-free-guidance forward (cond + a shorter, masked uncond
-    prompt) in ms ("cfg_batch2_ms"), and its 121 modulation linears' stacked
+    prompt) in ms ("cfg_batch2_ms", captured and replayed as a graph in
+    "cfg_batch2_graphed"), and its 121 modulation linears' stacked
     GEMV (2,217,984 x 3072 Q4_K) at M = 1 and 2 ("modulation_stack");
   * "cpu_baseline": candle's CPU QMatMul algorithm (quantize x to Q8_K,
     integer block dots, threads over output columns), restated as scalar C
@@ -719,12 +720,12 @@ def bench_stack(stack, ms_list, args):
     return out
 
 
-def bench_graphed(step, inp, n, eager_out):
+def bench_graphed(step, inp, n, eager_out, batched=False):
     """The same forward captured into a HIP graph (mold_amd.graphs.GraphedStep) and replayed:
     ms per step (median of n), and whether a replay equals the eager output bit for bit."""
     import torch
     from mold_amd.graphs import GraphedStep
-    g = GraphedStep(step, **inp)
+    g = GraphedStep(step, batched=batched, **inp)
     same = bool(torch.equal(g(**inp), eager_out))
     times = []
     for _ in range(n):
@@ -823,6 +824,9 @@ def bench_qwen(dev, args):
     assert torch.isfinite(outb).all().item(), "non-finite batched Qwen output"
     bms = sorted(btimes)[len(btimes) // 2]
     log(f"  CFG batch-2 forward {bms:.2f} ms (two batch-1 forwards: {2 * sorted(times)[len(times) // 2]:.2f} ms)")
+    bgraphed = bench_graphed(step, {"img": b_args[0], "txt": b_args[1], "t": b_args[2], "grid": b_args[3],
+                                    "txt_valid": [256, 180]}, len(btimes), outb, batched=True)
+    log(f"  graphed CFG batch-2 forward {bgraphed['ms']:.2f} ms, equals eager: {bgraphed['equals_eager']}")
     del outb, b_args, txt_u
     l_img = inp["grid"][0] * inp["grid"][1]
     lin, attn = Q.step_flop(cfg, l_img, 256)
@@ -835,7 +839,7 @@ def bench_qwen(dev, args):
            "graphed": graphed, "modulation_stack": stack,
            "tflops_linear_plus_attention": round((lin + attn) / (ms * 1e-3) / 1e12, 1),
            "flop_linear": lin, "flop_attention": attn,
-           "cfg_batch2_ms": round(bms, 3), "cfg_batch2_steps_timed": len(btimes),
+           "cfg_batch2_ms": round(bms, 3), "cfg_batch2_steps_timed": len(btimes), "cfg_batch2_graphed": bgraphed,
            "weight_bytes": params.quantized_bytes(), "attention": ATTENTION_BACKEND["name"],
            "config": f"Qwen-Image shape, 1328x1328, batch 1, {l_img} img + 256 txt tokens, 60 blocks; "
                      "q/k/v Q3_K (stacked per stream), MLP Q2_K, out-projections, modulation, stems Q4_K; "

@@ -18,8 +18,10 @@ row's valid-key share fell below flux.PAD_MIN_SHARE the step runs again eagerly
 with unpadded attention (exact), as `run_guarded` does for the eager forward.
 
 The output tensor belongs to the graph and is overwritten by the next replay.
-Non-tensor arguments (Qwen-Image's `grid`) and tensor shapes are fixed at
-capture.
+Non-tensor arguments (Qwen-Image's `grid`, the batched forward's `txt_valid`)
+and tensor shapes are fixed at capture.  With `batched=True` the captured
+forward is QwenImageStep.forward_batched (classifier-free guidance's cond and
+uncond in one batch-2 forward).
 """
 from __future__ import annotations
 
@@ -29,11 +31,16 @@ class GraphedStep:
     arguments of step.forward, e.g. flux.make_inputs(...)) captured into a HIP graph.
     Call it with inputs of the same shapes to run one forward."""
 
-    def __init__(self, step, **inputs):
+    def __init__(self, step, batched: bool = False, **inputs):
         import torch
         from .flux import attention_bf16
         self.step = step
+        self.batched = batched
         self.static = {k: (v.detach().clone() if torch.is_tensor(v) else v) for k, v in inputs.items()}
+        if batched:
+            b, lt = self.static["txt"].shape[0], self.static["txt"].shape[1]
+            tv = self.static.pop("txt_valid", None)
+            self.valid = [lt] * b if tv is None else [int(v) for v in tv]
         dev = next(v.device for v in self.static.values() if torch.is_tensor(v))
         self.guarded = step.attn is attention_bf16 and step.pad_attention
         self.guard = torch.zeros((), dtype=torch.float32, device=dev)
@@ -54,12 +61,22 @@ class GraphedStep:
 
     def _forward(self):
         self.guard.zero_()
-        return self.step._forward(**self.static, blocks=None)
+        return self._eager()
+
+    def _eager(self):
+        s = self.static
+        if self.batched:
+            return self.step._forward_batched(s["img"], s["txt"], s["t"], s["grid"], self.valid, None)
+        return self.step._forward(**s, blocks=None)
 
     def __call__(self, **inputs):
         import torch
         from .flux import PAD_MIN_SHARE
         for k, v in inputs.items():
+            if self.batched and k == "txt_valid":
+                if v is not None and [int(c) for c in v] != self.valid:
+                    raise ValueError(f"GraphedStep: txt_valid = {v!r}, captured {self.valid!r}")
+                continue
             s = self.static[k]
             if torch.is_tensor(v):
                 if v.shape != s.shape:
@@ -73,7 +90,7 @@ class GraphedStep:
             st = self.step
             st.pad_attention = False
             try:
-                return st._forward(**self.static, blocks=None)
+                return self._eager()
             finally:
                 st.pad_attention = True
         return self.out

@@ -74,3 +74,31 @@ def test_graphed_step_guard_reruns_unpadded(monkeypatch):
         step.pad_attention = True
     torch.cuda.synchronize()
     assert torch.equal(out, ref) and torch.equal(out, unpadded)
+
+
+def test_graphed_cfg_batch2_equals_eager_forward_batched():
+    """Qwen-Image's batched CFG forward (cond + a shorter, masked uncond prompt) captured
+    with batched=True: every replay equals the eager forward_batched bit for bit, and a
+    txt_valid other than the captured one is refused."""
+    from mold_amd.graphs import GraphedStep
+    print("[graphs] qwen CFG batch 2: capture, then replays against eager forward_batched", flush=True)
+    step, make = _steps()["qwen"]
+
+    def make2(seed):
+        inp = make(seed)
+        g = torch.Generator(device="cuda").manual_seed(100 + seed)
+        txt_u = torch.randn(inp["txt"].shape, device="cuda", generator=g)
+        txt_u[27:] = 0.0
+        return {"img": torch.stack([inp["img"], inp["img"]]), "txt": torch.stack([inp["txt"], txt_u]),
+                "t": torch.cat([inp["t"], inp["t"]]), "grid": inp["grid"], "txt_valid": [32, 27]}
+
+    g = GraphedStep(step, batched=True, **make2(1))
+    for seed in (2, 3):
+        inp = make2(seed)
+        out = g(**inp).clone()
+        ref = step.forward_batched(**inp)
+        torch.cuda.synchronize()
+        assert out.shape == ref.shape and torch.isfinite(out).all().item()
+        assert torch.equal(out, ref), seed
+    with pytest.raises(ValueError):
+        g(**{**make2(4), "txt_valid": [32, 26]})
