@@ -102,3 +102,24 @@ def test_graphed_cfg_batch2_equals_eager_forward_batched():
         assert torch.equal(out, ref), seed
     with pytest.raises(ValueError):
         g(**{**make2(4), "txt_valid": [32, 26]})
+
+
+def test_graphed_cfg_batch2_guard_reruns_unpadded(monkeypatch):
+    """The batched capture keeps the guard too: with every padded row tripping it, a replay
+    reruns forward_batched unpadded and equals the eager (also rerun) batched forward."""
+    from mold_amd.graphs import GraphedStep
+    step, make = _steps()["qwen"]
+    inp = make(1)
+    b = {"img": torch.stack([inp["img"], inp["img"]]), "txt": torch.stack([inp["txt"], inp["txt"]]),
+         "t": torch.cat([inp["t"], inp["t"]]), "grid": inp["grid"], "txt_valid": [32, 25]}
+    g = GraphedStep(step, batched=True, **b)
+    monkeypatch.setattr(F, "PAD_MIN_SHARE", 1.0)
+    out = g(**b).clone()
+    ref = step.forward_batched(**b)
+    step.pad_attention = False
+    try:
+        unpadded = step.forward_batched(**b)
+    finally:
+        step.pad_attention = True
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref) and torch.equal(out, unpadded)
