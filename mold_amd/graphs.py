@@ -38,9 +38,16 @@ class GraphedStep:
         self.batched = batched
         self.static = {k: (v.detach().clone() if torch.is_tensor(v) else v) for k, v in inputs.items()}
         if batched:
+            if not hasattr(step, "_forward_batched"):
+                raise ValueError(f"GraphedStep: {type(step).__name__} has no batched forward")
+            img = self.static["img"]
             b, lt = self.static["txt"].shape[0], self.static["txt"].shape[1]
+            if not step._fused(img.reshape(b * img.shape[1], -1)):
+                raise ValueError("GraphedStep: the batched forward runs on the GPU with bf16 GEMM inputs")
             tv = self.static.pop("txt_valid", None)
             self.valid = [lt] * b if tv is None else [int(v) for v in tv]
+            if len(self.valid) != b or any(v < 1 or v > lt for v in self.valid):
+                raise ValueError("GraphedStep: txt_valid needs one count in 1 .. L_txt per batch element")
         dev = next(v.device for v in self.static.values() if torch.is_tensor(v))
         self.guarded = step.attn is attention_bf16 and step.pad_attention
         self.guard = torch.zeros((), dtype=torch.float32, device=dev)

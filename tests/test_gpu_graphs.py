@@ -102,6 +102,9 @@ def test_graphed_cfg_batch2_equals_eager_forward_batched():
         assert torch.equal(out, ref), seed
     with pytest.raises(ValueError):
         g(**{**make2(4), "txt_valid": [32, 26]})
+    for bad in ([32, 0], [33, 27], [32]):     # no valid token, more than L_txt, one count for two
+        with pytest.raises(ValueError):
+            GraphedStep(step, batched=True, **{**make2(5), "txt_valid": bad})
 
 
 def test_graphed_cfg_batch2_guard_reruns_unpadded(monkeypatch):
